@@ -1,0 +1,108 @@
+"""Build recipe for the MI355X trie beam search libraries (in-tree).
+
+Outputs, next to this file:
+  libflashtrie_amd.so   C ABI + HIP kernels (hipcc, gfx950)
+  libmarisa_amd.so      drop-in marisa::Trie, image builder, generators (g++)
+  flashtrie*.so         the `flashtrie` Python module (pybind11)
+
+Run ``python flash-trie_amd/build.py`` or call ``build()``.
+"""
+
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+INC = os.path.join(ROOT, "include")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+ARCH = "gfx950"
+
+# Device flags: no packed-FP32 instruction selection, no FMA contraction (the
+# scores must round exactly like the reference's host arithmetic).
+HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
+             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang",
+             "-packed-fp32-ops", "-I" + INC, "-I" + CSRC]
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-ffp-contract=off",
+             "-Wall", "-Wno-unused-parameter", "-I" + INC, "-I" + CSRC]
+
+LIB_AMD = os.path.join(HERE, "libflashtrie_amd.so")
+LIB_MARISA = os.path.join(HERE, "libmarisa_amd.so")
+
+
+def ext_suffix():
+    return sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+
+
+PYMOD = os.path.join(HERE, "flashtrie" + ext_suffix())
+
+
+def _run(cmd):
+    p = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                       text=True)
+    out = "\n".join(l for l in p.stdout.splitlines()
+                    if "packed-fp32-ops" not in l)
+    if p.returncode != 0:
+        raise RuntimeError("build step failed: " + " ".join(cmd) + "\n" + out)
+    return out
+
+
+def _pybind_includes():
+    import pybind11
+    return ["-I" + pybind11.get_include(),
+            "-I" + sysconfig.get_paths()["include"]]
+
+
+def build(verbose=False):
+    os.makedirs(OBJ, exist_ok=True)
+    hip_objs = {
+        "tbs_kernel.hip": os.path.join(OBJ, "tbs_kernel.o"),
+        "ft_runtime.cpp": os.path.join(OBJ, "ft_runtime.o"),
+    }
+    host_objs = {
+        "marisa_trie.cc": os.path.join(OBJ, "marisa_trie.o"),
+        "image_builder.cc": os.path.join(OBJ, "image_builder.o"),
+        "synth.cc": os.path.join(OBJ, "synth.o"),
+    }
+    bind_obj = os.path.join(OBJ, "bindings.o")
+    jobs = []
+    for src, obj in hip_objs.items():
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        jobs.append([HIPCC] + HIP_FLAGS + lang + ["-c", os.path.join(CSRC, src),
+                                                  "-o", obj])
+    for src, obj in host_objs.items():
+        jobs.append([CXX] + CXX_FLAGS + ["-c", os.path.join(CSRC, src),
+                                         "-o", obj])
+    jobs.append([CXX] + CXX_FLAGS + _pybind_includes() +
+                ["-fvisibility=hidden", "-c", os.path.join(CSRC, "bindings.cc"),
+                 "-o", bind_obj])
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        outs = list(ex.map(_run, jobs))
+    if verbose:
+        for o in outs:
+            if o.strip():
+                print(o)
+    _run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", LIB_AMD]
+         + list(hip_objs.values()))
+    _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", LIB_MARISA]
+         + list(host_objs.values()) +
+         ["-L" + HERE, "-lflashtrie_amd", "-Wl,-rpath,$ORIGIN"])
+    _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", PYMOD, bind_obj,
+          "-L" + HERE, "-lmarisa_amd", "-lflashtrie_amd",
+          "-Wl,-rpath,$ORIGIN"])
+    return [LIB_AMD, LIB_MARISA, PYMOD]
+
+
+def built():
+    return all(os.path.exists(p) for p in (LIB_AMD, LIB_MARISA, PYMOD))
+
+
+if __name__ == "__main__":
+    for p in build(verbose="-v" in sys.argv):
+        print(p)

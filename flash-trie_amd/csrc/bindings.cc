@@ -1,0 +1,425 @@
+// bindings.cc -- the `flashtrie` Python module.
+//
+// Same names, arguments, defaults and return shapes as the reference module
+// (tools/bindings.cpp:24-122): Trie (load, mmap, build, total_size,
+// num_tries, num_keys, num_nodes, save, clear, init_tbs_gpu), tbs,
+// bs_tbs_gpu and load_topk_keys_and_scores.  Errors raise RuntimeError.
+//
+// Beyond the reference: numpy entry points used by the benchmark and tests
+// (build_arrays, image, stage / launch / sync / fetch, search_np) and the
+// seeded synthetic generators (synth_keys, synth_requests).
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <iostream>
+#include <numeric>
+#include <sstream>
+#include <thread>
+
+#include "../../include/flashtrie_amd.h"
+#include "image_builder.h"
+#include "marisa.h"
+#include "synth.h"
+#include "trie_impl.h"
+
+namespace py = pybind11;
+using marisa::Label;
+using marisa::TbsInput;
+using marisa::Trie;
+
+
+namespace {
+
+ft_ctx* ctx_of(const Trie& t) {
+  marisa::TrieImpl* im = t.impl();
+  if (!im || !im->ctx)
+    throw marisa::Exception(MARISA_STATE_ERROR, "init_tbs_gpu was not called");
+  return im->ctx;
+}
+
+const ftamd::ImageBlob& image_of(const Trie& t) {
+  marisa::TrieImpl* im = t.impl();
+  if (!im || im->img.empty())
+    throw marisa::Exception(MARISA_STATE_ERROR, "trie is not built or loaded");
+  return im->img;
+}
+
+void check_ft(int rc, const char* where) {
+  if (rc == FT_OK) return;
+  std::string msg = std::string(where) + ": " + ft_strerror(rc);
+  const char* d = ft_last_error();
+  if (d && *d) msg += std::string(" (") + d + ")";
+  throw marisa::Exception(MARISA_STATE_ERROR, msg);
+}
+
+// The reference's load_topk_keys_and_scores (tools/beam-search-helper.h:26-120):
+// first line of each file "num_requests max_output_len topk", then one line
+// per (request, depth); rows after depth 0 are re-sorted by token id.
+std::tuple<std::vector<std::vector<std::vector<Label>>>,
+           std::vector<std::vector<std::vector<float>>>>
+load_topk(const std::string& dir) {
+  const std::string kp = dir + "/topk_keys.txt", sp = dir + "/topk_scores.txt";
+  std::ifstream kf(kp), sf(sp);
+  if (!kf.is_open()) throw marisa::Exception(MARISA_IO_ERROR, "cannot open " + kp);
+  if (!sf.is_open()) throw marisa::Exception(MARISA_IO_ERROR, "cannot open " + sp);
+  std::string kl, sl, buf;
+  std::getline(kf, kl);
+  std::getline(sf, sl);
+  std::stringstream kss(kl), sss(sl);
+  uint32_t meta[3];
+  for (int i = 0; i < 3; ++i) {
+    if (!(kss >> buf)) throw marisa::Exception(MARISA_FORMAT_ERROR, "bad header in " + kp);
+    meta[i] = (uint32_t)std::stoi(buf);
+    if (!(sss >> buf) || (uint32_t)std::stoi(buf) != meta[i])
+      throw marisa::Exception(MARISA_FORMAT_ERROR, "headers of the two files differ");
+  }
+  const uint32_t nreq = meta[0], depth = meta[1], topk = meta[2];
+  std::vector<std::vector<std::vector<Label>>> keys(nreq);
+  std::vector<std::vector<std::vector<float>>> scores(nreq);
+  for (uint32_t r = 0; r < nreq; ++r) {
+    keys[r].resize(depth);
+    scores[r].resize(depth);
+    for (uint32_t d = 0; d < depth; ++d) {
+      auto& lk = keys[r][d];
+      auto& ls = scores[r][d];
+      std::getline(kf, kl);
+      std::stringstream ks(kl);
+      while (ks >> buf) lk.push_back(static_cast<Label>(std::stof(buf)));
+      std::getline(sf, sl);
+      std::stringstream ss(sl);
+      while (ss >> buf) ls.push_back(std::stof(buf));
+      if (lk.size() != topk || ls.size() != topk)
+        throw marisa::Exception(MARISA_FORMAT_ERROR, "row length differs from topk");
+      if (d > 0) {
+        std::vector<size_t> p(lk.size());
+        std::iota(p.begin(), p.end(), 0);
+        std::sort(p.begin(), p.end(), [&](size_t a, size_t b) { return lk[a] < lk[b]; });
+        std::vector<Label> k2(lk.size());
+        std::vector<float> s2(ls.size());
+        for (size_t i = 0; i < p.size(); ++i) {
+          k2[i] = lk[p[i]];
+          s2[i] = ls[p[i]];
+        }
+        lk.swap(k2);
+        ls.swap(s2);
+      }
+    }
+  }
+  return std::make_tuple(keys, scores);
+}
+
+// --- numpy batch staging (benchmark path) ----------------------------------
+struct NpBatch {
+  std::vector<ft_request> reqs;
+  std::vector<uint32_t> F, T;
+  uint32_t K = 0;
+};
+
+NpBatch& staged_batch() {
+  static NpBatch b;
+  return b;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(flashtrie, m) {
+  m.doc() = "MI355X trie beam search (drop-in for the reference flashtrie module)";
+  py::register_exception<marisa::Exception>(m, "MarisaError", PyExc_RuntimeError);
+
+  py::class_<Trie>(m, "Trie")
+      .def(py::init<>())
+      .def("load", [](Trie& t, const std::string& p) { t.load(p.c_str()); })
+      .def("mmap", [](Trie& t, const std::string& p) { t.mmap(p.c_str()); })
+      .def("build",
+           [](Trie& t, const std::vector<std::vector<uint32_t>>& rows) {
+             marisa::Keyset ks;
+             for (const auto& r : rows) ks.push_back(r.data(), r.size());
+             t.build(ks, 1 | MARISA_TEXT_TAIL | MARISA_LABEL_ORDER | MARISA_DEFAULT_CACHE);
+           },
+           py::arg("token_rows"))
+      .def("total_size", &Trie::total_size)
+      .def("num_tries", &Trie::num_tries)
+      .def("num_keys", &Trie::num_keys)
+      .def("num_nodes", &Trie::num_nodes)
+      .def("save", [](const Trie& t, const std::string& p) { t.save(p.c_str()); })
+      .def("clear", &Trie::clear)
+      .def("get_max_batch_size", &Trie::get_max_batch_size)
+      .def("init_tbs_gpu", &Trie::init_tbs_gpu, py::arg("max_batch_size"),
+           py::arg("max_num_topk") = 1024, py::arg("max_num_outpos") = 64,
+           py::arg("max_num_out_beams") = 8192,
+           py::arg("max_num_out_tokens") = 8192 * 64,
+           py::arg("max_num_inter_beams") = 1024 * 1024,
+           py::arg("radix_topk_threshold") = 1024)
+      // ---- beyond the reference ----
+      .def("build_arrays",
+           [](Trie& t, py::array_t<uint32_t, py::array::c_style | py::array::forcecast> toks,
+              py::array_t<uint64_t, py::array::c_style | py::array::forcecast> offs) {
+             if (offs.ndim() != 1 || offs.shape(0) < 1)
+               throw marisa::Exception(MARISA_CODE_ERROR, "offsets must be 1-D, length >= 1");
+             const uint64_t n = (uint64_t)offs.shape(0) - 1;
+             const uint64_t* o = offs.data();
+             if (o[0] != 0 || o[n] != (uint64_t)toks.size())
+               throw marisa::Exception(MARISA_CODE_ERROR, "offsets do not cover the tokens");
+             ftamd::ImageBlob img;
+             std::string err;
+             bool ok;
+             {
+               py::gil_scoped_release nogil;
+               ok = ftamd::build_image_from_keys(toks.data(), o, n, &img, &err);
+             }
+             if (!ok) throw marisa::Exception(MARISA_SIZE_ERROR, "build: " + err);
+             t.assign_image(img.data(), img.size());
+           },
+           py::arg("tokens"), py::arg("offsets"))
+      .def("image",
+           [](const Trie& t) {
+             const ftamd::ImageBlob& img = image_of(t);
+             return py::array_t<uint8_t>((py::ssize_t)img.size(), img.data());
+           })
+      .def("assign_image",
+           [](Trie& t, py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a) {
+             t.assign_image(a.data(), (size_t)a.size());
+           })
+      .def("device_info", [](const Trie& t) {
+        int cus = 0, lds = 0, khz = 0;
+        char name[64] = {0};
+        check_ft(ft_device_info(ctx_of(t), &cus, &lds, &khz, name, sizeof(name)),
+                 "device_info");
+        py::dict d;
+        d["num_cus"] = cus;
+        d["lds_per_block"] = lds;
+        d["wall_clock_khz"] = khz;
+        d["arch"] = std::string(name);
+        return d;
+      });
+
+  m.def(
+      "tbs",
+      [](Trie& trie, const std::vector<uint32_t>& beams,
+         const std::vector<std::vector<Label>>& topk_id,
+         const std::vector<std::vector<float>>& topk_logp,
+         float token_logp_threshold, double sent_logp_threshold,
+         double length_norm, bool early_exit, bool use_gpu) {
+        std::vector<std::vector<Label>> out_sent;
+        std::vector<double> out_logp_norm;
+        auto start = std::chrono::high_resolution_clock::now();
+        TbsInput input{beams, topk_id, topk_logp, out_sent, out_logp_norm,
+                       token_logp_threshold, sent_logp_threshold, length_norm,
+                       early_exit};
+        {
+          py::gil_scoped_release nogil;
+          if (use_gpu) trie.tbs_gpu(input); else trie.tbs(input);
+        }
+        auto end = std::chrono::high_resolution_clock::now();
+        return std::make_tuple(out_sent, out_logp_norm, marisa::get_msec(start, end));
+      },
+      py::arg("trie"), py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"),
+      py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
+      py::arg("length_norm"), py::arg("early_exit"), py::arg("use_gpu") = false);
+
+  m.def(
+      "bs_tbs_gpu",
+      [](Trie& trie, size_t batch_size,
+         const std::vector<std::vector<uint32_t>>& batch_beams,
+         const std::vector<std::vector<std::vector<Label>>>& batch_topk_id,
+         const std::vector<std::vector<std::vector<float>>>& batch_topk_logp,
+         float token_logp_threshold, double sent_logp_threshold,
+         double length_norm, bool early_exit) {
+        ctx_of(trie);  // init_tbs_gpu must have run
+        if (batch_size > trie.get_max_batch_size())
+          throw marisa::Exception(MARISA_BOUND_ERROR, "bs_tbs_gpu: batch_size > max_batch_size");
+        if (batch_size != batch_topk_id.size() || batch_size != batch_topk_logp.size() ||
+            batch_size != batch_beams.size())
+          throw marisa::Exception(MARISA_CODE_ERROR, "bs_tbs_gpu: batch_size does not match the inputs");
+        std::vector<TbsInput> inputs;
+        std::vector<std::vector<std::vector<Label>>> out_sent(batch_size);
+        std::vector<std::vector<double>> out_norm(batch_size);
+        auto start = std::chrono::high_resolution_clock::now();
+        for (size_t i = 0; i < batch_size; ++i)
+          inputs.push_back(TbsInput{batch_beams[i], batch_topk_id[i], batch_topk_logp[i],
+                                    out_sent[i], out_norm[i], token_logp_threshold,
+                                    sent_logp_threshold, length_norm, early_exit});
+        {
+          py::gil_scoped_release nogil;
+          trie.tbs_gpu_batched(inputs);
+        }
+        auto end = std::chrono::high_resolution_clock::now();
+        std::vector<std::vector<double>> phase;
+        for (auto& in : inputs)
+          phase.push_back({in.t_expansion_ms, in.t_validation_ms, in.t_selection_ms,
+                           in.t_grid_overhead_ms, in.kernel_ms});
+        return std::make_tuple(out_sent, out_norm, marisa::get_msec(start, end), phase);
+      },
+      py::arg("trie"), py::arg("batch_size"), py::arg("batch_beams"),
+      py::arg("batch_topk_id"), py::arg("batch_topk_logp"),
+      py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
+      py::arg("length_norm"), py::arg("early_exit"));
+
+  m.def("load_topk_keys_and_scores", &load_topk, py::arg("dataset_dir"));
+
+  // ---- numpy batch path: stage / launch / sync / fetch -----------------------
+  m.def(
+      "stage",
+      [](Trie& trie, py::array_t<uint32_t, py::array::c_style | py::array::forcecast> beams,
+         py::array_t<uint32_t, py::array::c_style | py::array::forcecast> ids,
+         py::array_t<float, py::array::c_style | py::array::forcecast> logp,
+         float token_logp_threshold, double sent_logp_threshold, double length_norm,
+         bool early_exit) {
+        // beams [B][T], ids / logp [B][T][K]
+        if (beams.ndim() != 2 || ids.ndim() != 3 || logp.ndim() != 3 ||
+            ids.shape(0) != beams.shape(0) || ids.shape(1) != beams.shape(1) ||
+            logp.shape(0) != ids.shape(0) || logp.shape(1) != ids.shape(1) ||
+            logp.shape(2) != ids.shape(2))
+          throw marisa::Exception(MARISA_CODE_ERROR, "stage: shapes must be [B][T], [B][T][K]");
+        ft_ctx* c = ctx_of(trie);
+        NpBatch& nb = staged_batch();
+        const size_t B = beams.shape(0), T = beams.shape(1), K = ids.shape(2);
+        nb.reqs.assign(B, ft_request{});
+        nb.F.assign(B, 0);
+        nb.T.assign(B, (uint32_t)T);
+        nb.K = (uint32_t)K;
+        for (size_t b = 0; b < B; ++b) {
+          ft_request& q = nb.reqs[b];
+          q.beams = beams.data() + b * T;
+          q.num_beams = (uint32_t)T;
+          q.num_steps = (uint32_t)T;
+          q.topk = (uint32_t)K;
+          q.topk_id = ids.data() + b * T * K;
+          q.topk_logp = logp.data() + b * T * K;
+          q.token_logp_threshold = token_logp_threshold;
+          q.sent_logp_threshold = sent_logp_threshold;
+          q.length_norm = length_norm;
+          q.early_exit = early_exit;
+          nb.F[b] = T ? q.beams[T - 1] : 0;
+        }
+        check_ft(ft_stage(c, nb.reqs.data(), B), "stage");
+      },
+      py::arg("trie"), py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"),
+      py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
+      py::arg("length_norm"), py::arg("early_exit"));
+  m.def("launch", [](Trie& trie) { check_ft(ft_launch(ctx_of(trie)), "launch"); });
+  m.def("sync", [](Trie& trie) {
+    double ms = 0.0;
+    {
+      py::gil_scoped_release nogil;
+      check_ft(ft_sync(ctx_of(trie), &ms), "sync");
+    }
+    return ms;
+  });
+  m.def("fetch", [](Trie& trie) {
+    // returns (count[B], norms[B][F], lengths[B][F], tokens[B][F][T], timing)
+    ft_ctx* c = ctx_of(trie);
+    NpBatch& nb = staged_batch();
+    const size_t B = nb.reqs.size();
+    uint32_t Fm = 1, Tm = 1;
+    for (size_t b = 0; b < B; ++b) {
+      Fm = std::max(Fm, nb.F[b]);
+      Tm = std::max(Tm, nb.T[b]);
+    }
+    py::array_t<uint32_t> count((py::ssize_t)B);
+    py::array_t<double> norms({(py::ssize_t)B, (py::ssize_t)Fm});
+    py::array_t<uint32_t> lens({(py::ssize_t)B, (py::ssize_t)Fm});
+    py::array_t<uint32_t> toks({(py::ssize_t)B, (py::ssize_t)Fm, (py::ssize_t)Tm});
+    py::array_t<double> dev({(py::ssize_t)B, (py::ssize_t)4});
+    std::memset(norms.mutable_data(), 0, B * Fm * 8);
+    std::memset(lens.mutable_data(), 0, B * Fm * 4);
+    std::memset(toks.mutable_data(), 0, B * Fm * Tm * 4);
+    std::vector<ft_result> res(B);
+    for (size_t b = 0; b < B; ++b) {
+      std::memset(&res[b], 0, sizeof(ft_result));
+      res[b].capacity = Fm;
+      res[b].token_stride = Tm;
+      res[b].logp_norm = norms.mutable_data() + b * Fm;
+      res[b].length = lens.mutable_data() + b * Fm;
+      res[b].tokens = toks.mutable_data() + b * Fm * Tm;
+    }
+    ft_timing tm{};
+    int rc;
+    {
+      py::gil_scoped_release nogil;
+      rc = ft_fetch(c, res.data(), B, &tm);
+    }
+    check_ft(rc, "fetch");
+    for (size_t b = 0; b < B; ++b) {
+      count.mutable_data()[b] = res[b].count;
+      for (int i = 0; i < 4; ++i) dev.mutable_data()[b * 4 + i] = res[b].device_ms[i];
+    }
+    py::dict d;
+    d["kernel_ms"] = tm.kernel_ms;
+    d["expand_ms"] = tm.expand_ms;
+    d["select_ms"] = tm.select_ms;
+    d["other_ms"] = tm.other_ms;
+    d["candidates"] = tm.candidates;
+    d["parents"] = tm.parents;
+    d["children"] = tm.children;
+    d["probes"] = tm.probes;
+    d["device_ms"] = dev;
+    return py::make_tuple(count, norms, lens, toks, d);
+  });
+
+  // ---- synthetic generators ----------------------------------------------------
+  m.def(
+      "synth_keys",
+      [](uint64_t n, uint32_t vocab, uint32_t lmin, uint32_t lmax, double s, uint64_t seed) {
+        std::vector<uint32_t> toks;
+        std::vector<uint64_t> offs;
+        {
+          py::gil_scoped_release nogil;
+          ftamd::synth::make_keys(n, vocab, lmin, lmax, s, seed, &toks, &offs);
+        }
+        py::array_t<uint32_t> t((py::ssize_t)toks.size());
+        py::array_t<uint64_t> o((py::ssize_t)offs.size());
+        if (!toks.empty()) std::memcpy(t.mutable_data(), toks.data(), toks.size() * 4);
+        std::memcpy(o.mutable_data(), offs.data(), offs.size() * 8);
+        return py::make_tuple(t, o);
+      },
+      py::arg("n"), py::arg("vocab"), py::arg("lmin"), py::arg("lmax"), py::arg("s"),
+      py::arg("seed"));
+  m.def(
+      "synth_requests",
+      [](const Trie& trie, uint64_t first, uint64_t count, uint32_t vocab, uint32_t steps,
+         uint32_t topk, uint32_t seed_paths, double seed_mass, double sigma,
+         bool analytic_rest, uint64_t seed, int threads) {
+        const ftamd::ImageBlob& img = image_of(trie);
+        ftamd::synth::ProposalSpec sp;
+        sp.vocab = vocab;
+        sp.steps = steps;
+        sp.topk = topk;
+        sp.seed_paths = seed_paths;
+        sp.seed_mass = seed_mass;
+        sp.sigma = sigma;
+        sp.analytic_rest = analytic_rest;
+        py::array_t<uint32_t> ids({(py::ssize_t)count, (py::ssize_t)steps, (py::ssize_t)topk});
+        py::array_t<float> lp({(py::ssize_t)count, (py::ssize_t)steps, (py::ssize_t)topk});
+        uint32_t* ip = ids.mutable_data();
+        float* fp = lp.mutable_data();
+        {
+          py::gil_scoped_release nogil;
+          int nt = threads > 0 ? threads : (int)std::max(1u, std::thread::hardware_concurrency());
+          nt = (int)std::min<uint64_t>((uint64_t)nt, std::max<uint64_t>(count, 1));
+          std::atomic<uint64_t> nextr{0};
+          std::vector<std::thread> pool;
+          for (int w = 0; w < nt; ++w)
+            pool.emplace_back([&]() {
+              for (;;) {
+                const uint64_t r = nextr.fetch_add(1);
+                if (r >= count) break;
+                ftamd::synth::make_request(img, sp, seed, first + r,
+                                           ip + r * steps * topk, fp + r * steps * topk);
+              }
+            });
+          for (auto& th : pool) th.join();
+        }
+        return py::make_tuple(ids, lp);
+      },
+      py::arg("trie"), py::arg("first"), py::arg("count"), py::arg("vocab"),
+      py::arg("steps"), py::arg("topk"), py::arg("seed_paths"), py::arg("seed_mass"),
+      py::arg("sigma"), py::arg("analytic_rest"), py::arg("seed"), py::arg("threads") = 0);
+}

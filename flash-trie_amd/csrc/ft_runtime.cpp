@@ -1,0 +1,522 @@
+// ft_runtime.cpp -- host side of the C ABI (include/flashtrie_amd.h).
+//
+// Owns the trie image in HBM, the per-request workspace (allocated once by
+// ft_reserve, like LoudsTrie::init_tbs_gpu, tbs-kernels.cu:599-648), the
+// pinned staging buffers and the stream.  A batch is packed into one pinned
+// buffer, copied with one H2D, searched by one cooperative launch and copied
+// back with one D2H (compare the per-request launches of tbs_gpu_batched,
+// tbs-kernels.cu:686-700).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "../../include/flashtrie_amd.h"
+#include "tbs_kernel.h"
+
+using namespace ftk;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorOutOfMemory ? FT_E_NOMEM : FT_E_HIP;
+}
+
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+struct StagedReq {
+  uint32_t T = 0, K = 0, F = 0;
+  bool skip = false;
+  uint64_t out_bytes = 0;
+};
+
+}  // namespace
+
+struct ft_ctx {
+  int device = 0;
+  uint8_t* d_image = nullptr;
+  ft_image_header hdr{};
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  int num_cus = 0, lds_per_block = 0, wall_khz = 0;
+  char name[64] = {0};
+
+  bool reserved = false;
+  size_t max_batch = 0, max_topk = 0, max_steps = 0, max_out_beams = 0,
+         max_out_tokens = 0, max_inter = 0;
+  WsLayout lay{};
+  uint64_t ws_stride = 0;
+  uint8_t* d_ws = nullptr;
+  uint64_t out_slot_max = 0;
+  uint8_t* d_out = nullptr;
+  uint8_t* h_out = nullptr;
+  uint64_t stage_cap = 0;
+  uint8_t* d_stage = nullptr;
+  uint8_t* h_stage = nullptr;
+
+  std::vector<StagedReq> staged;
+  uint64_t out_stride = 0;
+  bool launched = false;
+  uint32_t scan_mult = 8;
+};
+
+static void release_workspace(ft_ctx* c) {
+  if (c->d_ws) (void)hipFree(c->d_ws);
+  if (c->d_out) (void)hipFree(c->d_out);
+  if (c->d_stage) (void)hipFree(c->d_stage);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->h_stage) (void)hipHostFree(c->h_stage);
+  c->d_ws = c->d_out = c->d_stage = c->h_out = c->h_stage = nullptr;
+  c->reserved = false;
+}
+
+extern "C" {
+
+const char* ft_last_error(void) { return g_err.c_str(); }
+
+const char* ft_strerror(int code) {
+  switch (code) {
+    case FT_OK: return "ok";
+    case FT_E_ARG: return "invalid argument";
+    case FT_E_NOMEM: return "out of memory";
+    case FT_E_HIP: return "HIP runtime error";
+    case FT_E_LIMIT: return "request exceeds the reserved workspace";
+    case FT_E_STATE: return "call sequence error (init_tbs_gpu / stage missing)";
+    case FT_E_INPUT: return "malformed request";
+    case FT_E_IMAGE: return "malformed trie image";
+    case FT_E_DEVICE: return "no usable gfx950 device";
+    case FT_E_KERNEL: return "search kernel reported an internal error";
+    default: return "unknown error";
+  }
+}
+
+int ft_create(const void* image, size_t image_bytes, int device,
+              ft_ctx** out) {
+  if (!image || !out || image_bytes < sizeof(ft_image_header))
+    return fail(FT_E_ARG, "ft_create: null image or too small");
+  *out = nullptr;
+  ft_image_header h;
+  std::memcpy(&h, image, sizeof(h));
+  if (std::memcmp(h.magic, FT_IMAGE_MAGIC, 7) != 0)
+    return fail(FT_E_IMAGE, "ft_create: bad image magic");
+  if (h.total_bytes != image_bytes || h.num_nodes == 0 ||
+      h.num_nodes >= 0xFFFFFFFFull ||
+      h.recs_offset + (h.num_nodes + 1) * sizeof(ft_node_rec) > image_bytes ||
+      h.parent_offset + h.num_nodes * 4 > image_bytes ||
+      h.tail_offset + h.tail_len * 4 > image_bytes || h.recs_offset % 16)
+    return fail(FT_E_IMAGE, "ft_create: inconsistent image header");
+
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess || ndev <= device || device < 0)
+    return fail(FT_E_DEVICE, "ft_create: no HIP device " + std::to_string(device));
+  if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+    return hip_fail(e, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(FT_E_DEVICE, std::string("ft_create: device is ") +
+                                 prop.gcnArchName + ", this build targets gfx950");
+  int coop = 0;
+  (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
+  if (!coop) return fail(FT_E_DEVICE, "ft_create: no cooperative launch");
+
+  auto* c = new ft_ctx();
+  c->device = device;
+  c->hdr = h;
+  c->num_cus = prop.multiProcessorCount;
+  c->lds_per_block = (int)prop.sharedMemPerBlock;
+  int wc = 0;
+  (void)hipDeviceGetAttribute(&wc, hipDeviceAttributeWallClockRate, device);
+  c->wall_khz = wc;
+  std::snprintf(c->name, sizeof(c->name), "%s", prop.gcnArchName);
+  if ((e = hipMalloc(&c->d_image, image_bytes)) != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipMalloc(image)");
+  }
+  if ((e = hipMemcpy(c->d_image, image, image_bytes, hipMemcpyHostToDevice)) !=
+      hipSuccess) {
+    (void)hipFree(c->d_image);
+    delete c;
+    return hip_fail(e, "hipMemcpy(image)");
+  }
+  if ((e = hipStreamCreate(&c->stream)) != hipSuccess) {
+    (void)hipFree(c->d_image);
+    delete c;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  (void)hipEventCreate(&c->ev0);
+  (void)hipEventCreate(&c->ev1);
+  if (const char* s = std::getenv("FT_SCAN_MULT")) {
+    const long v = std::strtol(s, nullptr, 10);
+    if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
+  }
+  *out = c;
+  return FT_OK;
+}
+
+int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
+               size_t max_out_beams, size_t max_out_tokens,
+               size_t max_inter_beams) {
+  if (!c) return fail(FT_E_ARG, "ft_reserve: null context");
+  if (max_batch == 0 || max_topk == 0 || max_steps == 0 ||
+      max_out_beams == 0 || max_out_tokens == 0 || max_inter_beams == 0)
+    return fail(FT_E_ARG, "ft_reserve: every limit must be positive");
+  if (max_topk > kMaxLdsTopk)
+    return fail(FT_E_LIMIT, "ft_reserve: max_num_topk " +
+                                std::to_string(max_topk) + " > " +
+                                std::to_string(kMaxLdsTopk));
+  if (max_out_beams > kMaxBeams)
+    return fail(FT_E_LIMIT, "ft_reserve: max_num_out_beams > 65535");
+  if (max_steps > 16383)
+    return fail(FT_E_LIMIT, "ft_reserve: max_num_outpos > 16383");
+  if (max_inter_beams >= 0xFFFFFFF0ull)
+    return fail(FT_E_LIMIT, "ft_reserve: max_num_inter_beams too large");
+  (void)hipSetDevice(c->device);
+  release_workspace(c);
+  const uint64_t B = max_out_beams, K = max_topk;
+  const uint64_t BK = B * K;
+  if (BK + B >= 0xFFFFFFF0ull) return fail(FT_E_LIMIT, "ft_reserve: beams * topk too large");
+  WsLayout L{};
+  uint64_t off = 0;
+  L.cur0 = off; off = align_up(off + B * sizeof(CurRec), 256);
+  L.cur1 = off; off = align_up(off + B * sizeof(CurRec), 256);
+  L.nextc = off; off = align_up(off + BK * sizeof(NextRec), 256);
+  L.selA = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
+  L.selB = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
+  L.rank = off; off = align_up(off + B * 4, 256);
+  L.hist = off; off = align_up(off + (uint64_t)max_inter_beams * sizeof(HistRec), 256);
+  L.next_cap = (uint32_t)BK;
+  L.sel_cap = (uint32_t)(BK + B);
+  L.hist_cap = (uint32_t)max_inter_beams;
+  L.cur_cap = (uint32_t)B;
+  c->lay = L;
+  c->ws_stride = off;
+  c->out_slot_max = align_up(sizeof(OutHeader) + 12 * B + 4 * (uint64_t)max_out_tokens, 256);
+  // per request: lnf + beams + ids + logps + row flags + permutation
+  const uint64_t per_req = align_up(8 * (max_steps + 1), 16) +
+                           align_up(4 * max_steps, 16) +
+                           3 * align_up(4 * max_steps * K, 16) +
+                           align_up(max_steps, 16) + 256;
+  c->stage_cap = align_up(max_batch * sizeof(DevReq), 256) + max_batch * per_req;
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_ws, c->ws_stride * max_batch)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipMalloc(workspace)");
+  if ((e = hipMalloc(&c->d_out, c->out_slot_max * max_batch)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipMalloc(output)");
+  if ((e = hipMalloc(&c->d_stage, c->stage_cap)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipMalloc(stage)");
+  if ((e = hipHostMalloc(&c->h_out, c->out_slot_max * max_batch, 0)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipHostMalloc(output)");
+  if ((e = hipHostMalloc(&c->h_stage, c->stage_cap, 0)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipHostMalloc(stage)");
+  c->max_batch = max_batch;
+  c->max_topk = max_topk;
+  c->max_steps = max_steps;
+  c->max_out_beams = max_out_beams;
+  c->max_out_tokens = max_out_tokens;
+  c->max_inter = max_inter_beams;
+  c->reserved = true;
+  c->staged.clear();
+  c->launched = false;
+  return FT_OK;
+}
+
+int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
+  if (!c || (!reqs && batch)) return fail(FT_E_ARG, "ft_stage: null argument");
+  if (!c->reserved) return fail(FT_E_STATE, "ft_stage: init_tbs_gpu (ft_reserve) was not called");
+  if (batch == 0 || batch > c->max_batch)
+    return fail(FT_E_LIMIT, "ft_stage: batch size " + std::to_string(batch) +
+                                " not in [1, max_batch_size=" +
+                                std::to_string(c->max_batch) + "]");
+  c->staged.assign(batch, StagedReq());
+  c->launched = false;
+  uint8_t* H = c->h_stage;
+  DevReq* D = (DevReq*)H;
+  uint64_t off = align_up(batch * sizeof(DevReq), 256);
+  uint64_t max_out = sizeof(OutHeader);
+  std::vector<std::pair<uint32_t, uint32_t>> tmp;
+  for (size_t r = 0; r < batch; ++r) {
+    const ft_request& q = reqs[r];
+    const std::string who = "request " + std::to_string(r) + ": ";
+    DevReq d{};
+    StagedReq& st = c->staged[r];
+    if (q.num_beams == 0 || !q.beams)
+      return fail(FT_E_INPUT, who + "beams is empty");
+    const uint32_t F = q.beams[q.num_beams - 1];
+    if (F == 0) {  // outputs untouched (louds-trie.cc:114-117)
+      st.skip = true;
+      d.flags = kReqSkip;
+      d.in_off = off;
+      D[r] = d;
+      continue;
+    }
+    const uint32_t T = q.num_steps, K = q.topk;
+    if (T == 0 || K == 0)
+      return fail(FT_E_INPUT, who + "topk rows are empty");
+    if (q.num_beams < T)
+      return fail(FT_E_INPUT, who + "fewer beam widths than topk rows");
+    if (T > c->max_steps)
+      return fail(FT_E_LIMIT, who + "steps " + std::to_string(T) +
+                                  " > max_num_outpos " + std::to_string(c->max_steps));
+    if (K > c->max_topk)
+      return fail(FT_E_LIMIT, who + "topk " + std::to_string(K) +
+                                  " > max_num_topk " + std::to_string(c->max_topk));
+    if (F > c->max_out_beams)
+      return fail(FT_E_LIMIT, who + "final beam > max_num_out_beams");
+    if ((uint64_t)F * T > c->max_out_tokens)
+      return fail(FT_E_LIMIT, who + "final beam * steps > max_num_out_tokens");
+    for (uint32_t t = 0; t < T; ++t) {
+      if (q.beams[t] == 0)
+        return fail(FT_E_INPUT, who + "beam width 0 at step " + std::to_string(t));
+      if (q.beams[t] > c->max_out_beams)
+        return fail(FT_E_LIMIT, who + "beam width > max_num_out_beams");
+    }
+    if (!q.topk_id_rows && (!q.topk_id || !q.topk_logp))
+      return fail(FT_E_ARG, who + "null topk arrays");
+    if (q.topk_id_rows && !q.topk_logp_rows)
+      return fail(FT_E_ARG, who + "null topk_logp rows");
+    d.T = T;
+    d.K = K;
+    d.F = F;
+    d.flags = q.early_exit ? kReqEarlyExit : 0u;
+    d.tok_thr = q.token_logp_threshold;
+    d.sent_thr = q.sent_logp_threshold;
+    d.in_off = off;
+    d.out_T = T;
+    uint8_t* base = H + off;
+    uint64_t o = 0;
+    // length-norm table, exactly Agent::logp_norm's factor (agent.h:69-72)
+    double* lnf = (double*)(base + o);
+    for (uint32_t dd = 0; dd <= T; ++dd) {
+      lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
+      if (!std::isfinite(lnf[dd]))
+        return fail(FT_E_INPUT, who + "length_norm gives a non-finite factor");
+    }
+    o = align_up(o + 8ull * (T + 1), 16);
+    d.beams_off = (uint32_t)o;
+    std::memcpy(base + o, q.beams, 4ull * T);
+    o = align_up(o + 4ull * T, 16);
+    d.ids_off = (uint32_t)o;
+    uint32_t* ids = (uint32_t*)(base + o);
+    o = align_up(o + 4ull * T * K, 16);
+    d.lp_off = (uint32_t)o;
+    float* lps = (float*)(base + o);
+    o = align_up(o + 4ull * T * K, 16);
+    d.rowflag_off = (uint32_t)o;
+    uint8_t* rowflag = base + o;
+    o = align_up(o + T, 16);
+    bool any_perm = false;
+    for (uint32_t t = 0; t < T; ++t) {
+      const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
+      const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
+      if (!rid || !rlp) return fail(FT_E_ARG, who + "null topk row");
+      std::memcpy(ids + (uint64_t)t * K, rid, 4ull * K);
+      std::memcpy(lps + (uint64_t)t * K, rlp, 4ull * K);
+      bool sorted = true;
+      for (uint32_t k = 0; k < K; ++k) {
+        const float x = rlp[k];
+        if (std::isnan(x) || x == std::numeric_limits<float>::infinity())
+          return fail(FT_E_INPUT, who + "topk_logp holds NaN or +inf");
+        if (k && rid[k] <= rid[k - 1]) sorted = false;
+      }
+      rowflag[t] = sorted ? 0 : 1;
+      any_perm |= !sorted;
+    }
+    d.perm_off = 0;
+    if (any_perm) {
+      d.perm_off = (uint32_t)o;
+      uint32_t* perm = (uint32_t*)(base + o);
+      o = align_up(o + 4ull * T * K, 16);
+      for (uint32_t t = 0; t < T; ++t) {
+        if (!rowflag[t]) continue;
+        const uint32_t* rid = ids + (uint64_t)t * K;
+        tmp.resize(K);
+        for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
+        std::sort(tmp.begin(), tmp.end());
+        for (uint32_t k = 0; k < K; ++k) {
+          if (k && tmp[k].first == tmp[k - 1].first)
+            return fail(FT_E_INPUT, who + "duplicate token id " +
+                                        std::to_string(tmp[k].first) +
+                                        " in topk row " + std::to_string(t));
+          perm[(uint64_t)t * K + k] = tmp[k].second;
+        }
+      }
+    }
+    off = align_up(off + o, 256);
+    if (off > c->stage_cap) return fail(FT_E_LIMIT, "ft_stage: staging overflow");
+    st.T = T;
+    st.K = K;
+    st.F = F;
+    st.out_bytes = sizeof(OutHeader) + 12ull * F + 4ull * F * T;
+    max_out = std::max(max_out, st.out_bytes);
+    D[r] = d;
+  }
+  c->out_stride = align_up(max_out, 256);
+  (void)hipSetDevice(c->device);
+  hipError_t e = hipMemcpyAsync(c->d_stage, c->h_stage, off, hipMemcpyHostToDevice, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(stage)");
+  return FT_OK;
+}
+
+int ft_launch(ft_ctx* c) {
+  if (!c) return fail(FT_E_ARG, "ft_launch: null context");
+  if (c->staged.empty()) return fail(FT_E_STATE, "ft_launch: nothing staged");
+  KArgs a{};
+  a.recs = (const ft_node_rec*)(c->d_image + c->hdr.recs_offset);
+  a.parent = (const uint32_t*)(c->d_image + c->hdr.parent_offset);
+  a.tail = (const uint32_t*)(c->d_image + c->hdr.tail_offset);
+  a.reqs = (const DevReq*)c->d_stage;
+  a.stage = c->d_stage;
+  a.ws = c->d_ws;
+  a.ws_stride = c->ws_stride;
+  a.out = c->d_out;
+  a.out_stride = c->out_stride;
+  a.lay = c->lay;
+  a.batch = (uint32_t)c->staged.size();
+  uint32_t kmax = 1;
+  for (auto& s : c->staged) kmax = std::max(kmax, s.K);
+  const uint64_t sl = (uint64_t)c->scan_mult * kmax;
+  a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
+  (void)hipSetDevice(c->device);
+  (void)hipEventRecord(c->ev0, c->stream);
+  hipError_t e = launch_tbs(a, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel");
+  (void)hipEventRecord(c->ev1, c->stream);
+  c->launched = true;
+  return FT_OK;
+}
+
+int ft_sync(ft_ctx* c, double* ms) {
+  if (!c) return fail(FT_E_ARG, "ft_sync: null context");
+  (void)hipSetDevice(c->device);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  if (ms) {
+    float f = 0.f;
+    (void)hipEventElapsedTime(&f, c->ev0, c->ev1);
+    *ms = f;
+  }
+  return FT_OK;
+}
+
+int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
+  if (!c) return fail(FT_E_ARG, "ft_fetch: null context");
+  if (!c->launched) return fail(FT_E_STATE, "ft_fetch: no launch to fetch");
+  if (batch != c->staged.size()) return fail(FT_E_ARG, "ft_fetch: batch mismatch");
+  (void)hipSetDevice(c->device);
+  hipError_t e = hipMemcpyAsync(c->h_out, c->d_out, c->out_stride * batch,
+                                hipMemcpyDeviceToHost, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(output)");
+  double ms = 0.0;
+  int rc = ft_sync(c, &ms);
+  if (rc) return rc;
+  int first_err = FT_OK;
+  ft_timing tm{};
+  tm.kernel_ms = ms;
+  const double tick_ms = c->wall_khz > 0 ? 1.0 / c->wall_khz : 0.0;
+  for (size_t r = 0; r < batch; ++r) {
+    const StagedReq& st = c->staged[r];
+    ft_result& o = res[r];
+    if (st.skip) {
+      o.count = 0;
+      o.status = FT_OK;
+      continue;
+    }
+    const uint8_t* ob = c->h_out + c->out_stride * r;
+    const OutHeader* oh = (const OutHeader*)ob;
+    tm.expand_ms += oh->ticks_expand * tick_ms;
+    tm.select_ms += oh->ticks_select * tick_ms;
+    tm.other_ms += (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
+    tm.candidates += oh->candidates;
+    tm.parents += oh->parents;
+    tm.children += oh->children;
+    tm.probes += oh->probes;
+    if (oh->status) {
+      o.count = 0;
+      o.status = (oh->status & kStatusHistory) ? FT_E_LIMIT : FT_E_KERNEL;
+      if (!first_err) {
+        first_err = o.status;
+        g_err = "request " + std::to_string(r) +
+                ((oh->status & kStatusHistory)
+                     ? ": hypotheses exceed max_num_inter_beams"
+                     : ": kernel status " + std::to_string(oh->status));
+      }
+      continue;
+    }
+    const uint32_t n = oh->count;
+    if (n > o.capacity || (n && (!o.logp_norm || !o.length || !o.tokens)) ||
+        o.token_stride < st.T) {
+      o.count = 0;
+      o.status = FT_E_ARG;
+      if (!first_err) {
+        first_err = FT_E_ARG;
+        g_err = "request " + std::to_string(r) + ": result arrays too small";
+      }
+      continue;
+    }
+    o.device_ms[0] = oh->ticks_expand * tick_ms;
+    o.device_ms[1] = oh->ticks_select * tick_ms;
+    o.device_ms[2] = (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
+    o.device_ms[3] = oh->ticks_total * tick_ms;
+    const double* norms = (const double*)(ob + sizeof(OutHeader));
+    const uint32_t* lens = (const uint32_t*)(norms + st.F);
+    const uint32_t* toks = lens + st.F;
+    std::memcpy(o.logp_norm, norms, 8ull * n);
+    std::memcpy(o.length, lens, 4ull * n);
+    for (uint32_t i = 0; i < n; ++i) {
+      const uint32_t L = std::min(lens[i], st.T);
+      std::memcpy(o.tokens + (uint64_t)i * o.token_stride, toks + (uint64_t)i * st.T, 4ull * L);
+    }
+    o.count = n;
+    o.status = FT_OK;
+  }
+  if (timing) *timing = tm;
+  return first_err;
+}
+
+int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
+              ft_result* results, ft_timing* timing) {
+  int rc = ft_stage(c, reqs, batch);
+  if (rc) return rc;
+  rc = ft_launch(c);
+  if (rc) return rc;
+  return ft_fetch(c, results, batch, timing);
+}
+
+void ft_destroy(ft_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  release_workspace(c);
+  if (c->d_image) (void)hipFree(c->d_image);
+  if (c->ev0) (void)hipEventDestroy(c->ev0);
+  if (c->ev1) (void)hipEventDestroy(c->ev1);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int ft_device_info(ft_ctx* c, int* num_cus, int* lds_per_block,
+                   int* wall_clock_khz, char* name, size_t name_len) {
+  if (!c) return fail(FT_E_ARG, "ft_device_info: null context");
+  if (num_cus) *num_cus = c->num_cus;
+  if (lds_per_block) *lds_per_block = c->lds_per_block;
+  if (wall_clock_khz) *wall_clock_khz = c->wall_khz;
+  if (name && name_len) std::snprintf(name, name_len, "%s", c->name);
+  return FT_OK;
+}
+
+}  // extern "C"

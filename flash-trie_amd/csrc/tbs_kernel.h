@@ -1,0 +1,103 @@
+// tbs_kernel.h -- structures shared by the TBS kernel and its host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flashtrie_amd.h"
+
+namespace ftk {
+
+// Largest K whose proposal row is staged in LDS (10 bytes per proposal).
+constexpr uint32_t kMaxLdsTopk = 4096;
+// Parent index and proposal index are packed into 16 bits each.
+constexpr uint32_t kMaxBeams = 65535;
+constexpr uint32_t kNoHist = 0xFFFFFFFFu;
+
+enum : uint32_t { kReqEarlyExit = 1u, kReqSkip = 2u };
+
+enum : uint32_t {
+  kStatusOverflow = 1u,  // candidate buffer too small (never expected)
+  kStatusHistory = 2u,   // history capacity (max_num_inter_beams) exceeded
+  kStatusCorrupt = 4u,   // a link-parent walk did not terminate
+};
+
+// Per-request descriptor, packed by the host at the start of the staging
+// buffer.  Offsets are relative to in_off.
+struct DevReq {
+  uint32_t T, K, F, flags;
+  float tok_thr;
+  uint32_t pad0;
+  double sent_thr;
+  uint64_t in_off;     // byte offset of this request's block in the stage
+  uint32_t beams_off;  // lnf[T + 1] (f64) sits at offset 0
+  uint32_t ids_off;
+  uint32_t lp_off;
+  uint32_t rowflag_off;  // uint8_t[T]: 1 if row t is permuted
+  uint32_t perm_off;     // uint32_t[T * K] or 0
+  uint32_t out_T;        // token stride of the output rows
+};
+
+struct CurRec {     // a hypothesis kept in the beam
+  double s;         // f64 sum of logps
+  uint32_t node;
+  uint32_t hist;    // its history record (kNoHist for the root)
+};
+
+struct NextRec {    // a push into `next`
+  uint64_t key;     // order-preserving norm
+  uint32_t node;
+  uint32_t jk;      // parent slot << 16 | proposal index
+};
+
+struct SelRec {     // a push into `selected`
+  double s;
+  uint32_t node;
+  uint32_t depth;   // |Q|
+  uint32_t phist;   // history record of the parent
+  uint32_t tok;     // last token
+  uint32_t jk;
+  uint32_t isnew;   // pushed during the current step
+};
+
+struct HistRec {
+  uint32_t phist;
+  uint32_t tok;
+};
+
+struct OutHeader {  // 64 bytes, then norms[F] f64, lengths[F], tokens[F*T]
+  uint32_t count;
+  uint32_t status;
+  uint64_t ticks_expand, ticks_select, ticks_total;
+  uint64_t candidates, parents, children, probes;
+};
+static_assert(sizeof(OutHeader) == 64, "OutHeader layout");
+
+struct WsLayout {   // byte offsets inside one request's workspace slot
+  uint64_t cur0, cur1, nextc, selA, selB, rank, hist;
+  uint32_t next_cap, sel_cap, hist_cap, cur_cap;
+};
+
+struct KArgs {
+  const ft_node_rec* recs;
+  const uint32_t* parent;
+  const uint32_t* tail;
+  const DevReq* reqs;
+  const uint8_t* stage;
+  uint8_t* ws;
+  uint64_t ws_stride;
+  uint8_t* out;
+  uint64_t out_stride;
+  WsLayout lay;
+  uint32_t batch;
+  uint32_t scan_limit;
+};
+
+// Launches the search over `batch` requests (one workgroup each) as a
+// cooperative launch on `stream`.
+hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
+
+// Threads per workgroup of the search kernel.
+int tbs_block_threads();
+
+}  // namespace ftk

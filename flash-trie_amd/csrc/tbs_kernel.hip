@@ -1,0 +1,768 @@
+// tbs_kernel.hip -- trie beam search (TBS) kernel for gfx950 (MI355X).
+//
+// One persistent workgroup of 1024 threads (16 wave64) runs the complete
+// search of one request: every decoding step's expansion, validation and
+// pruning, with the whole batch in a single cooperative launch and no host
+// round trip between steps.  Semantics are those of the reference CPU path
+// LoudsTrie::tbs (lib/marisa/grimoire/trie/louds-trie.cc:75-177):
+//
+//  * cur is processed parent by parent in ascending (norm, node id) order and
+//    each parent's proposals in index order; a parent is a "link parent" when
+//    terminal(n) and |KB| > |Q| (louds-trie.cc:151-153), and then only the
+//    token KB(n)[|Q|] can extend it (louds-trie.cc:91-102);
+//  * otherwise the child whose first edge token equals the proposal is
+//    taken (predictive_find_child, louds-trie.cc:810-856); it goes to
+//    `selected` if terminal with |KB| == |Q| and always to `next`
+//    (louds-trie.cc:103-108);
+//  * `next` and `selected` are bounded heaps (candidates.h:32-80).
+//
+// The bounded heaps are reproduced exactly without a sequential heap.  For
+// pushes e_1..e_n (arrival order) into a heap of capacity M with keys
+// (norm, node id) -- node ids are distinct inside every heap -- the final
+// content is:
+//    n <= M: everything;
+//    else with v* = the M-th largest norm, G = #{norm > v*}, r = M - G:
+//      all items with norm > v*, plus, among A = the norm == v* items that
+//      are among the first M items (in arrival order) of {norm >= v*}, the r
+//      with the largest node ids.
+// Arrival order is (parent rank in ascending (norm, node), proposal index);
+// it is only computed when the boundary norm v* is tied (E > r) or when
+// early exit truncates `selected` to the first F pushes.
+//
+// Scores: s is the f64 sum of f32 logps (agent.cc:36); norm = s * lnf[|Q|]
+// with lnf[d] = pow(6 / (5 + d), alpha) computed on the host with the same
+// libm call as the reference (agent.h:69-72), so norms are bit-identical.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "tbs_kernel.h"
+
+namespace ftk {
+
+constexpr int kBlock = 1024;
+constexpr int kWaves = kBlock / 64;
+
+struct Smem {
+  // expansion: the current proposal row in ascending token order
+  uint32_t row_id[kMaxLdsTopk];
+  float row_lp[kMaxLdsTopk];
+  uint16_t row_k[kMaxLdsTopk];
+  // expansion: one chunk of up to kBlock parents
+  uint32_t woff[kBlock + 1];
+  uint32_t pc0[kBlock];
+  uint32_t paux[kBlock];
+  uint32_t pnode[kBlock];
+  uint8_t pmode[kBlock];
+  // selection
+  uint32_t hist[256];
+  uint32_t wsum[kWaves];
+  uint32_t sel_digit, sel_cum, sel_cnt;
+  uint32_t n_next, n_sel, n_out, overflow;
+  uint32_t status;
+  unsigned long long cnt_parents, cnt_children, cnt_probes;
+};
+// rank scratch aliases the row arrays (used after expansion only)
+constexpr int kRankChunk = 1024;
+
+enum : uint8_t {
+  M_NONE = 0,
+  M_LP_NEXT = 1,
+  M_LP_SEL = 2,
+  M_SCAN = 3,
+  M_SEARCH = 4
+};
+
+__device__ __forceinline__ uint64_t norm_key(double v) {
+  // order-preserving map of a double to uint64; -0.0 and +0.0 are equal
+  if (v == 0.0) v = 0.0;
+  uint64_t b = (uint64_t)__double_as_longlong(v);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ uint32_t lanemask_lt_count(uint64_t m) {
+  const uint32_t lane = lane_id();
+  return (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+}
+
+// Wave-aggregated append: returns this lane's slot (valid if `want`).
+__device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
+  const uint64_t m = __ballot(want);
+  if (m == 0) return 0;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  uint32_t base = 0;
+  if ((int)lane_id() == leader) base = atomicAdd(ctr, (uint32_t)__popcll(m));
+  base = __shfl(base, leader, 64);
+  return base + lanemask_lt_count(m);
+}
+
+// Exclusive block scan of v over all kBlock threads.
+__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, Smem& sm) {
+  const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o, 64);
+    if (lane >= (uint32_t)o) x += y;
+  }
+  if (lane == 63) sm.wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t w = lane < (uint32_t)kWaves ? sm.wsum[lane] : 0;
+    uint32_t z = w;
+#pragma unroll
+    for (int o = 1; o < kWaves; o <<= 1) {
+      const uint32_t y = __shfl_up(z, o, 64);
+      if (lane >= (uint32_t)o) z += y;
+    }
+    if (lane < (uint32_t)kWaves) sm.wsum[lane] = z - w;  // exclusive
+    if (lane == (uint32_t)kWaves - 1) sm.sel_cum = z;      // grand total
+  }
+  __syncthreads();
+  const uint32_t r = x - v + sm.wsum[wave];
+  *total = sm.sel_cum;
+  __syncthreads();
+  return r;
+}
+
+// Adds 1 to hist[digit] for every active lane; lanes of a wave that agree on
+// the digit are merged into one LDS atomic.
+__device__ __forceinline__ void hist_add(bool act, uint32_t digit,
+                                         uint32_t* hist) {
+  const uint64_t am = __ballot(act);
+  if (am == 0) return;
+  const int leader = __ffsll((unsigned long long)am) - 1;
+  const uint32_t d0 = __shfl(digit, leader, 64);
+  const uint64_t same = __ballot(act && digit == d0);
+  if (same == am) {
+    if ((int)lane_id() == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(am));
+  } else if (act) {
+    atomicAdd(&hist[digit], 1u);
+  }
+}
+
+// Picks the bin holding the `rem`-th smallest item (1-based) from
+// sm.hist[256]; writes sel_digit / sel_cum (items in lower bins) / sel_cnt.
+__device__ void hist_pick(uint32_t rem, Smem& sm) {
+  if (threadIdx.x < 64) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t h0 = sm.hist[4 * lane], h1 = sm.hist[4 * lane + 1],
+                   h2 = sm.hist[4 * lane + 2], h3 = sm.hist[4 * lane + 3];
+    const uint32_t own = h0 + h1 + h2 + h3;
+    uint32_t x = own;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(x, o, 64);
+      if (lane >= (uint32_t)o) x += y;
+    }
+    const uint64_t hit = __ballot(x >= rem);
+    const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+    if ((int)lane == first) {
+      uint32_t cum = x - own;
+      uint32_t b = 4 * lane;
+      const uint32_t hs[4] = {h0, h1, h2, h3};
+      int i = 0;
+      for (; i < 3; ++i) {
+        if (cum + hs[i] >= rem) break;
+        cum += hs[i];
+      }
+      sm.sel_digit = b + i;
+      sm.sel_cum = cum;
+      sm.sel_cnt = hs[i];
+    }
+  }
+  __syncthreads();
+}
+
+// Radix selection of the `need`-th smallest key (1-based) among items
+// i < n with filt(i).  Returns it; *eq = items equal to it, *rem = how many
+// of those are needed to reach `need`.
+template <typename KeyT, typename GetKey, typename Filt>
+__device__ KeyT radix_kth(uint32_t n, uint32_t need, GetKey gk, Filt filt,
+                          Smem& sm, uint32_t* eq, uint32_t* rem_out) {
+  constexpr int kBits = (int)sizeof(KeyT) * 8;
+  KeyT prefix = 0, mask = 0;
+  uint32_t rem = need, cnt = 0;
+  for (int shift = kBits - 8; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += kBlock) sm.hist[i] = 0;
+    __syncthreads();
+    for (uint32_t base = 0; base < n; base += kBlock) {
+      const uint32_t i = base + threadIdx.x;
+      bool act = false;
+      uint32_t dg = 0;
+      if (i < n && filt(i)) {
+        const KeyT k = gk(i);
+        if ((k & mask) == prefix) {
+          act = true;
+          dg = (uint32_t)((k >> shift) & 0xFF);
+        }
+      }
+      hist_add(act, dg, sm.hist);
+    }
+    __syncthreads();
+    hist_pick(rem, sm);
+    prefix |= (KeyT)sm.sel_digit << shift;
+    mask |= (KeyT)0xFF << shift;
+    rem -= sm.sel_cum;
+    cnt = sm.sel_cnt;
+    __syncthreads();
+  }
+  *eq = cnt;
+  *rem_out = rem;
+  return prefix;
+}
+
+// Thresholds of the bounded-heap emulation (see the file comment).
+struct Bound {
+  uint64_t vkey;   // boundary key
+  uint32_t tie;    // 1 if the boundary class is cut
+  uint32_t astar;  // arrival cutoff (tie only)
+  uint32_t nustar; // node-id cutoff (tie only)
+  uint32_t all;    // 1 if everything survives
+};
+
+__device__ __forceinline__ bool bound_keep(const Bound& b, uint64_t key,
+                                           uint32_t arr, uint32_t node) {
+  if (b.all) return true;
+  if (key > b.vkey) return true;
+  if (key != b.vkey) return false;
+  if (!b.tie) return true;
+  return arr <= b.astar && node >= b.nustar;
+}
+
+// Bounded heap of capacity M over n items (see the file comment).  key(i),
+// arr(i) and node(i) read the items; arr() is only called on the tie path,
+// after `need_ranks()` has made parent ranks available.
+template <typename GetKey, typename GetArr, typename GetNode, typename Ranks>
+__device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
+                                GetArr arr, GetNode node, Ranks need_ranks,
+                                Smem& sm) {
+  Bound b{0, 0, 0, 0, 0};
+  if (n <= M) {
+    b.all = 1;
+    return b;
+  }
+  uint32_t eq, rem;
+  // M-th largest key == M-th smallest of ~key
+  const uint64_t nk = radix_kth<uint64_t>(
+      n, M, [&](uint32_t i) { return ~key(i); },
+      [&](uint32_t) { return true; }, sm, &eq, &rem);
+  b.vkey = ~nk;
+  if (eq == rem) return b;  // the whole boundary class fits
+  b.tie = 1;
+  need_ranks();
+  const uint64_t vk = b.vkey;
+  // first M of {key >= v*} in arrival order
+  uint32_t eq2, rem2;
+  b.astar = radix_kth<uint32_t>(
+      n, M, [&](uint32_t i) { return arr(i); },
+      [&](uint32_t i) { return key(i) >= vk; }, sm, &eq2, &rem2);
+  const uint32_t as = b.astar;
+  // the `rem` largest node ids of A
+  uint32_t eq3, rem3;
+  const uint32_t nn = radix_kth<uint32_t>(
+      n, rem, [&](uint32_t i) { return ~node(i); },
+      [&](uint32_t i) { return key(i) == vk && arr(i) <= as; }, sm, &eq3,
+      &rem3);
+  b.nustar = ~nn;
+  return b;
+}
+
+// KB(n)[j] for a link parent: walk up until the edge that covers position j.
+__device__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node_rec r,
+                             uint32_t j, uint32_t* err) {
+  for (int guard = 0; guard < 65536; ++guard) {
+    const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
+    const uint32_t el = (r.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+    const uint32_t start = sd - el;
+    if (j >= start) {
+      if (r.meta & FT_META_LINK) return a.tail[(uint64_t)r.tail_off + (j - start)];
+      return r.first_tok;
+    }
+    if (n == 0) break;
+    n = a.parent[n];
+    r = a.recs[n];
+  }
+  *err = 1;
+  return 0xFFFFFFFFu;
+}
+
+// position of tok in the sorted LDS row, or -1
+__device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
+                                        uint32_t tok) {
+  uint32_t lo = 0, hi = K;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (sm.row_id[mid] < tok) lo = mid + 1; else hi = mid;
+  }
+  return (lo < K && sm.row_id[lo] == tok) ? (int)lo : -1;
+}
+
+__global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
+  __shared__ Smem sm;
+  const uint32_t req = blockIdx.x;
+  const uint32_t tid = threadIdx.x;
+  if (req >= a.batch) return;
+
+  const DevReq d = a.reqs[req];
+  uint8_t* ws = a.ws + (uint64_t)req * a.ws_stride;
+  uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
+  OutHeader* oh = (OutHeader*)ob;
+  if (d.flags & kReqSkip) {
+    if (tid == 0) { oh->count = 0; oh->status = 0; }
+    return;
+  }
+  const uint8_t* in = a.stage + d.in_off;
+  const double* lnf = (const double*)in;
+  const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
+  const uint32_t* ids = (const uint32_t*)(in + d.ids_off);
+  const float* lps = (const float*)(in + d.lp_off);
+  const uint32_t* perm = d.perm_off ? (const uint32_t*)(in + d.perm_off) : nullptr;
+  const uint8_t* rowflag = in + d.rowflag_off;
+  const uint32_t T = d.T, K = d.K, F = d.F;
+  const bool early = (d.flags & kReqEarlyExit) != 0;
+
+  CurRec* cur = (CurRec*)(ws + a.lay.cur0);
+  CurRec* cur2 = (CurRec*)(ws + a.lay.cur1);
+  NextRec* nextc = (NextRec*)(ws + a.lay.nextc);
+  SelRec* selA = (SelRec*)(ws + a.lay.selA);
+  SelRec* selB = (SelRec*)(ws + a.lay.selB);
+  uint32_t* rank = (uint32_t*)(ws + a.lay.rank);
+  HistRec* hist = (HistRec*)(ws + a.lay.hist);
+  const uint32_t next_cap = a.lay.next_cap, sel_cap = a.lay.sel_cap,
+                 hist_cap = a.lay.hist_cap;
+
+  unsigned long long t_exp = 0, t_sel = 0, t_all0 = wall_clock64();
+  if (tid == 0) {
+    cur[0].s = 0.0;
+    cur[0].node = 0;
+    cur[0].hist = kNoHist;
+    sm.status = 0;
+    sm.cnt_parents = sm.cnt_children = sm.cnt_probes = 0;
+  }
+  uint32_t n_cur = 1, nS = 0, hist_used = 0;
+  uint64_t n_cands = 0;
+  __syncthreads();
+
+  for (uint32_t t = 0; t < T; ++t) {
+    if (n_cur == 0 || (early && nS >= F)) break;
+    const unsigned long long t0 = wall_clock64();
+    // ---- row t into LDS, ascending token order -------------------------
+    const uint32_t* rid = ids + (uint64_t)t * K;
+    const float* rlp = lps + (uint64_t)t * K;
+    const bool permuted = perm && rowflag[t] != 0;
+    for (uint32_t p = tid; p < K; p += kBlock) {
+      const uint32_t k = permuted ? perm[(uint64_t)t * K + p] : p;
+      sm.row_id[p] = rid[k];
+      sm.row_lp[p] = rlp[k];
+      sm.row_k[p] = (uint16_t)k;
+    }
+    if (tid == 0) {
+      sm.n_next = 0;
+      sm.n_sel = 0;
+      sm.overflow = 0;
+    }
+    const double lnf_next = lnf[t + 1];
+    __syncthreads();
+
+    // ---- expansion ------------------------------------------------------
+    for (uint32_t cbase = 0; cbase < n_cur; cbase += kBlock) {
+      const uint32_t j = cbase + tid;
+      uint32_t work = 0;
+      uint8_t mode = M_NONE;
+      if (j < n_cur) {
+        const CurRec p = cur[j];
+        const ft_node_rec r = a.recs[p.node];
+        const uint32_t cend = a.recs[p.node + 1].child_begin;
+        const uint32_t deg = cend - r.child_begin;
+        const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
+        uint32_t aux = deg;
+        if ((r.meta & FT_META_TERMINAL) && sd > t) {
+          uint32_t err = 0;
+          aux = kb_token(a, p.node, r, t, &err);
+          if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
+          mode = (t + 1 == sd) ? M_LP_SEL : M_LP_NEXT;
+          work = 1;
+        } else if (deg == 0) {
+          mode = M_NONE;
+        } else if (deg <= a.scan_limit) {
+          mode = M_SCAN;
+          work = deg;
+        } else {
+          mode = M_SEARCH;
+          work = K;
+        }
+        sm.pc0[tid] = r.child_begin;
+        sm.paux[tid] = aux;
+        sm.pnode[tid] = p.node;
+      }
+      sm.pmode[tid] = mode;
+      uint32_t W;
+      const uint32_t off = block_excl_scan(work, &W, sm);
+      sm.woff[tid] = off;
+      if (tid == 0) sm.woff[kBlock] = W;
+      if (tid == 0) sm.cnt_parents += min(n_cur - cbase, (uint32_t)kBlock);
+      __syncthreads();
+      const uint32_t nchunk = min(n_cur - cbase, (uint32_t)kBlock);
+      uint32_t my_children = 0, my_probes = 0;
+      for (uint32_t wbase = 0; wbase < W; wbase += kBlock) {
+        const uint32_t w = wbase + tid;
+        bool do_next = false, do_sel = false;
+        uint32_t cnode = 0, jj = 0, k = 0, tok = 0;
+        double s2 = 0.0;
+        uint32_t cdepth = t + 1;
+        if (w < W) {
+          // parent of work item w: last jj with woff[jj] <= w
+          uint32_t lo = 0, hi = nchunk;
+          while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (sm.woff[mid] <= w) lo = mid; else hi = mid;
+          }
+          jj = lo;
+          const uint32_t q = w - sm.woff[jj];
+          const uint8_t md = sm.pmode[jj];
+          const uint32_t pj = cbase + jj;
+          int pos = -1;
+          ft_node_rec cr;
+          bool have_child = false;
+          if (md == M_LP_NEXT || md == M_LP_SEL) {
+            pos = row_find(sm, K, sm.paux[jj]);
+            cnode = sm.pnode[jj];
+          } else if (md == M_SCAN) {
+            cnode = sm.pc0[jj] + q;
+            cr = a.recs[cnode];
+            ++my_children;
+            pos = row_find(sm, K, cr.first_tok);
+            have_child = true;
+          } else if (md == M_SEARCH) {
+            pos = (int)q;
+          }
+          if (pos >= 0) {
+            const float x = sm.row_lp[pos];
+            k = sm.row_k[pos];
+            tok = sm.row_id[pos];
+            const double ps = cur[pj].s;
+            const bool low = ((double)x <= (double)d.tok_thr) ||
+                             (ps + (double)x <= d.sent_thr);
+            if (!low) {
+              s2 = ps + (double)x;
+              if (md == M_SEARCH) {
+                // lower_bound of tok among the parent's children
+                uint32_t lo2 = sm.pc0[jj], hi2 = sm.pc0[jj] + sm.paux[jj];
+                const uint32_t end2 = hi2;
+                while (lo2 < hi2) {
+                  const uint32_t mid = lo2 + ((hi2 - lo2) >> 1);
+                  ++my_probes;
+                  if (a.recs[mid].first_tok < tok) lo2 = mid + 1; else hi2 = mid;
+                }
+                if (lo2 < end2) {
+                  cr = a.recs[lo2];
+                  if (cr.first_tok == tok) {
+                    cnode = lo2;
+                    have_child = true;
+                  }
+                }
+              }
+              if (md == M_LP_NEXT) {
+                do_next = true;
+              } else if (md == M_LP_SEL) {
+                do_sel = true;
+              } else if (have_child) {
+                do_next = true;
+                do_sel = (cr.meta & FT_META_TERMINAL) &&
+                         ((cr.meta & FT_META_DEPTH_MASK) == t + 1);
+              }
+            }
+          }
+        }
+        // appends (all lanes of the wave reach these)
+        const uint32_t jk = ((cbase + jj) << 16) | k;
+        const uint32_t in_ = wave_append(do_next, &sm.n_next);
+        if (do_next) {
+          if (in_ < next_cap) {
+            NextRec nr;
+            nr.key = norm_key(s2 * lnf_next);
+            nr.node = cnode;
+            nr.jk = jk;
+            nextc[in_] = nr;
+          } else {
+            atomicOr(&sm.overflow, 1u);
+          }
+        }
+        const uint32_t is_ = wave_append(do_sel, &sm.n_sel);
+        if (do_sel) {
+          const uint32_t slot = nS + is_;
+          if (slot < sel_cap) {
+            SelRec sr;
+            sr.s = s2;
+            sr.node = cnode;
+            sr.depth = cdepth;
+            sr.phist = cur[cbase + jj].hist;
+            sr.tok = tok;
+            sr.jk = jk;
+            sr.isnew = 1;
+            selA[slot] = sr;
+          } else {
+            atomicOr(&sm.overflow, 1u);
+          }
+        }
+      }
+      if (my_children) atomicAdd(&sm.cnt_children, (unsigned long long)my_children);
+      if (my_probes) atomicAdd(&sm.cnt_probes, (unsigned long long)my_probes);
+      __syncthreads();
+    }
+    const uint32_t n_next = sm.n_next, n_new = sm.n_sel;
+    n_cands += (uint64_t)n_next + n_new;
+    if (sm.overflow || sm.status) {
+      if (tid == 0) sm.status |= sm.overflow ? kStatusOverflow : 0u;
+      __syncthreads();
+      break;
+    }
+    const unsigned long long t1 = wall_clock64();
+    t_exp += t1 - t0;
+
+    // ---- parent ranks (only when arrival order is needed) ---------------
+    bool ranks_done = false;
+    const double lnf_cur = lnf[t];
+    const uint32_t ncur_now = n_cur;
+    auto compute_ranks = [&]() {
+      if (ranks_done) return;
+      ranks_done = true;
+      uint64_t* rk_key = (uint64_t*)sm.row_id;  // aliases the row (done)
+      uint32_t* rk_node = (uint32_t*)sm.row_lp;
+      __syncthreads();
+      for (uint32_t jb = 0; jb < ncur_now; jb += kBlock) {
+        const uint32_t j = jb + tid;
+        uint64_t myk = 0;
+        uint32_t myn = 0, cntless = 0;
+        if (j < ncur_now) {
+          myk = norm_key(cur[j].s * lnf_cur);
+          myn = cur[j].node;
+        }
+        for (uint32_t ib = 0; ib < ncur_now; ib += kRankChunk) {
+          const uint32_t i = ib + tid;
+          if (tid < (uint32_t)kRankChunk) {
+            if (i < ncur_now) {
+              rk_key[tid] = norm_key(cur[i].s * lnf_cur);
+              rk_node[tid] = cur[i].node;
+            }
+          }
+          __syncthreads();
+          const uint32_t m = min((uint32_t)kRankChunk, ncur_now - ib);
+          if (j < ncur_now) {
+            for (uint32_t q = 0; q < m; ++q) {
+              const uint64_t kk = rk_key[q];
+              cntless += (kk < myk) || (kk == myk && rk_node[q] < myn);
+            }
+          }
+          __syncthreads();
+        }
+        if (j < ncur_now) rank[j] = cntless;
+      }
+      __syncthreads();
+    };
+
+    // ---- selected ----------------------------------------------------------
+    bool stop_after = false;
+    if (n_new > 0) {
+      const uint32_t nU = nS + n_new;
+      auto sel_key = [&](uint32_t i) {
+        const SelRec& r = selA[i];
+        return norm_key(r.s * lnf[r.depth]);
+      };
+      auto sel_arr = [&](uint32_t i) {
+        const SelRec& r = selA[i];
+        if (!r.isnew) return 0u;
+        return 1u + rank[r.jk >> 16] * K + (r.jk & 0xFFFFu);
+      };
+      auto sel_node = [&](uint32_t i) { return selA[i].node; };
+      Bound b{0, 0, 0, 0, 1};
+      bool early_cut = false;
+      uint32_t acut = 0;
+      if (early) {
+        if (nU >= F) {
+          // the first F - nS new pushes in arrival order, then stop
+          compute_ranks();
+          const uint32_t want = F - nS;
+          uint32_t e1, r1;
+          acut = radix_kth<uint32_t>(
+              nU, want, [&](uint32_t i) { return sel_arr(i); },
+              [&](uint32_t i) { return i >= nS; }, sm, &e1, &r1);
+          early_cut = true;
+          stop_after = true;
+        }
+      } else {
+        b = bounded_select(nU, F, sel_key, sel_arr, sel_node, compute_ranks, sm);
+      }
+      if (b.all && !early_cut) {
+        // every push fits: the new items simply become old ones
+        for (uint32_t i = nS + tid; i < nU; i += kBlock) selA[i].isnew = 0;
+        nS = nU;
+      } else {
+        if (tid == 0) sm.n_out = 0;
+        __syncthreads();
+        for (uint32_t base = 0; base < nU; base += kBlock) {
+          const uint32_t i = base + tid;
+          bool keep = false;
+          if (i < nU) {
+            if (early_cut) keep = (i < nS) || sel_arr(i) <= acut;
+            else keep = bound_keep(b, sel_key(i), b.tie ? sel_arr(i) : 0u, sel_node(i));
+          }
+          const uint32_t o = wave_append(keep, &sm.n_out);
+          if (keep && o < sel_cap) {
+            SelRec r = selA[i];
+            r.isnew = 0;
+            selB[o] = r;
+          }
+        }
+        __syncthreads();
+        nS = sm.n_out;
+        SelRec* tmp = selA; selA = selB; selB = tmp;
+        if (nS > F) {  // the bound keeps at most F
+          if (tid == 0) sm.status |= kStatusCorrupt;
+          __syncthreads();
+          break;
+        }
+      }
+      __syncthreads();
+    }
+    if (stop_after) {
+      t_sel += wall_clock64() - t1;
+      break;
+    }
+
+    // ---- next --------------------------------------------------------------
+    const uint32_t M = beams[t];
+    auto nk = [&](uint32_t i) { return nextc[i].key; };
+    auto na = [&](uint32_t i) {
+      const uint32_t jk = nextc[i].jk;
+      return rank[jk >> 16] * K + (jk & 0xFFFFu);
+    };
+    auto nn = [&](uint32_t i) { return nextc[i].node; };
+    const Bound bn = bounded_select(n_next, M, nk, na, nn, compute_ranks, sm);
+    if (tid == 0) sm.n_out = 0;
+    __syncthreads();
+    const uint32_t keep_cnt = bn.all ? n_next : M;
+    if (hist_used + keep_cnt > hist_cap) {
+      if (tid == 0) sm.status |= kStatusHistory;
+      __syncthreads();
+      break;
+    }
+    for (uint32_t base = 0; base < n_next; base += kBlock) {
+      const uint32_t i = base + tid;
+      bool keep = false;
+      NextRec c;
+      if (i < n_next) {
+        c = nextc[i];
+        keep = bound_keep(bn, c.key, bn.tie ? na(i) : 0u, c.node);
+      }
+      const uint32_t o = wave_append(keep, &sm.n_out);
+      if (keep && o < a.lay.cur_cap && hist_used + o < hist_cap) {
+        const uint32_t j = c.jk >> 16, k = c.jk & 0xFFFFu;
+        const CurRec p = cur[j];
+        CurRec q;
+        q.s = p.s + (double)lps[(uint64_t)t * K + k];
+        q.node = c.node;
+        q.hist = hist_used + o;
+        cur2[o] = q;
+        HistRec h;
+        h.phist = p.hist;
+        h.tok = ids[(uint64_t)t * K + k];
+        hist[hist_used + o] = h;
+      }
+    }
+    __syncthreads();
+    n_cur = sm.n_out;
+    if (n_cur != keep_cnt) {  // the bound must keep exactly keep_cnt
+      if (tid == 0) sm.status |= kStatusCorrupt;
+      __syncthreads();
+      break;
+    }
+    hist_used += n_cur;
+    {
+      CurRec* tmp = cur; cur = cur2; cur2 = tmp;
+    }
+    t_sel += wall_clock64() - t1;
+    __syncthreads();
+  }
+
+  // ---- output: selected in ascending (norm, node id) -----------------------
+  const unsigned long long t2 = wall_clock64();
+  double* onorm = (double*)(ob + sizeof(OutHeader));
+  uint32_t* olen = (uint32_t*)(onorm + F);
+  uint32_t* otok = olen + F;
+  const uint32_t status = sm.status;
+  if (status == 0) {
+    uint64_t* rk_key = (uint64_t*)sm.row_id;
+    uint32_t* rk_node = (uint32_t*)sm.row_lp;
+    for (uint32_t jb = 0; jb < nS; jb += kBlock) {
+      const uint32_t j = jb + tid;
+      uint64_t myk = 0;
+      uint32_t myn = 0, cntless = 0;
+      SelRec me;
+      if (j < nS) {
+        me = selA[j];
+        myk = norm_key(me.s * lnf[me.depth]);
+        myn = me.node;
+      }
+      for (uint32_t ib = 0; ib < nS; ib += kRankChunk) {
+        const uint32_t i = ib + tid;
+        __syncthreads();
+        if (tid < (uint32_t)kRankChunk && i < nS) {
+          const SelRec o = selA[i];
+          rk_key[tid] = norm_key(o.s * lnf[o.depth]);
+          rk_node[tid] = o.node;
+        }
+        __syncthreads();
+        const uint32_t m = min((uint32_t)kRankChunk, nS - ib);
+        if (j < nS) {
+          for (uint32_t q = 0; q < m; ++q) {
+            const uint64_t kk = rk_key[q];
+            cntless += (kk < myk) || (kk == myk && rk_node[q] < myn);
+          }
+        }
+      }
+      if (j < nS && cntless < F) {
+        onorm[cntless] = me.s * lnf[me.depth];
+        olen[cntless] = me.depth;
+        uint32_t* row = otok + (uint64_t)cntless * d.out_T;
+        if (me.depth >= 1 && me.depth <= d.out_T) {
+          row[me.depth - 1] = me.tok;
+          uint32_t h = me.phist;
+          for (int pos = (int)me.depth - 2; pos >= 0; --pos) {
+            if (h >= hist_cap) break;
+            const HistRec hr = hist[h];
+            row[pos] = hr.tok;
+            h = hr.phist;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    oh->count = status ? 0 : nS;
+    oh->status = status;
+    const unsigned long long tend = wall_clock64();
+    oh->ticks_expand = t_exp;
+    oh->ticks_select = t_sel;
+    oh->ticks_total = tend - t_all0;
+    oh->candidates = n_cands;
+    oh->parents = sm.cnt_parents;
+    oh->children = sm.cnt_children;
+    oh->probes = sm.cnt_probes;
+    (void)t2;
+  }
+}
+
+hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
+  void* params[] = {(void*)&args};
+  return hipLaunchCooperativeKernel((const void*)tbs_kernel, dim3(args.batch),
+                                    dim3(kBlock), params, 0, stream);
+}
+
+int tbs_block_threads() { return kBlock; }
+
+}  // namespace ftk

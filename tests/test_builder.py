@@ -1,0 +1,109 @@
+"""The product's image builder against the oracle's restated MARISA build:
+same node ids, edges, terminals; image invariants; save / load."""
+
+import os
+
+import numpy as np
+import pytest
+from hypothesis import given, settings, strategies as st
+
+from helpers import decode_image, image_logical, oracle_logical
+
+
+def _same_trie(ft, po, keys=None, toks=None, offs=None):
+    t = ft.Trie()
+    if keys is not None:
+        t.build(keys)
+        o = po.OracleTrie.from_keys(keys)
+    else:
+        t.build_arrays(toks, offs)
+        o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    a = image_logical(t.image())
+    b = oracle_logical(o)
+    assert np.array_equal(a[0], b[0])
+    assert a[1] == b[1]
+    assert np.array_equal(a[2], b[2])
+    assert t.num_keys() == o.num_keys()
+    assert t.num_nodes() == o.num_nodes()
+    return t
+
+
+@settings(max_examples=80, deadline=None)
+@given(st.lists(st.lists(st.integers(0, 7), min_size=0, max_size=7),
+                min_size=1, max_size=50))
+def test_matches_oracle_small(ft, po, keys):
+    _same_trie(ft, po, keys=keys)
+
+
+def test_matches_oracle_synthetic(ft, po):
+    toks, offs = ft.synth_keys(30000, 4096, 3, 8, 1.1, 11)
+    assert len(offs) - 1 == 30000
+    _same_trie(ft, po, toks=toks, offs=offs)
+
+
+def test_empty_key_and_duplicates(ft, po):
+    _same_trie(ft, po, keys=[[], [1], [1], [1, 2], []])
+
+
+def test_image_fields(ft):
+    t = ft.Trie()
+    t.build([[1, 2, 3, 4], [1, 2, 3, 5], [7]])
+    n, recs, parent, tail = decode_image(t.image())
+    assert n == 5
+    meta = recs["meta"]
+    depth = meta & 0xFFFF
+    elen = (meta >> 16) & 0x3FFF
+    assert depth[:5].tolist() == [0, 3, 1, 4, 4]
+    assert elen[:5].tolist() == [0, 3, 1, 1, 1]
+    assert parent.tolist() == [0, 0, 0, 1, 1]
+    assert tail[recs["tail_off"][1]:recs["tail_off"][1] + 3].tolist() == [1, 2, 3]
+    assert recs["child_begin"][5] == 5   # sentinel
+
+
+def test_rejects_large_token(ft):
+    t = ft.Trie()
+    with pytest.raises(RuntimeError, match="2\\^31"):
+        t.build([[1, 2 ** 31]])
+
+
+def test_save_load_roundtrip(ft, tmp_path):
+    t = ft.Trie()
+    t.build([[3, 1], [3, 2, 9], [4]])
+    p = str(tmp_path / "trie.ftimg")
+    t.save(p)
+    u = ft.Trie()
+    u.load(p)
+    assert np.array_equal(t.image(), u.image())
+    assert u.num_keys() == 3 and u.num_tries() == 1
+    m = ft.Trie()
+    m.mmap(p)
+    assert np.array_equal(t.image(), m.image())
+
+
+def test_load_rejects_marisa_file(ft, tmp_path):
+    p = tmp_path / "trie.bin"
+    p.write_bytes(b"We love Marisa." + b"\0" * 64)
+    with pytest.raises(RuntimeError, match="MARISA"):
+        ft.Trie().load(str(p))
+
+
+def test_load_rejects_corrupt_image(ft, tmp_path):
+    t = ft.Trie()
+    t.build([[3, 1], [3, 2, 9], [4]])
+    img = t.image().copy()
+    _, recs, _, _ = decode_image(img)
+    ro = 256
+    img[ro + 16 + 0] = 0   # node 1's child_begin -> 0 (not BFS)
+    p = tmp_path / "bad.ftimg"
+    p.write_bytes(img.tobytes())
+    with pytest.raises(RuntimeError):
+        ft.Trie().load(str(p))
+
+
+def test_uninitialised_trie_errors(ft):
+    t = ft.Trie()
+    with pytest.raises(RuntimeError):
+        t.num_keys()
+    t.build([[1]])
+    with pytest.raises(RuntimeError, match="init_tbs_gpu"):
+        ft.bs_tbs_gpu(t, 1, [[1]], [[[1]]], [[[-1.0]]], -10, -40, 5, False)

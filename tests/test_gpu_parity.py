@@ -1,0 +1,242 @@
+"""GPU parity: the HIP search (through flashtrie -> the C ABI) against the CPU
+oracle on identical seeded inputs.  Sequences and lengths bit-exact; scores
+within 1e-5 relative (they are in fact bit-identical: the length-norm
+factor comes from a host pow table and the f64 additions are the same)."""
+
+import math
+
+import numpy as np
+import pytest
+
+from helpers import assert_same_results, load_golden
+
+pytestmark = pytest.mark.gpu
+
+KA = load_golden("known_answers.json")
+
+
+def _gpu_trie(ft, keys=None, toks=None, offs=None, batch=8, topk=64, steps=16,
+              beams=64, inter=1 << 16):
+    t = ft.Trie()
+    if keys is not None:
+        t.build(keys)
+    else:
+        t.build_arrays(toks, offs)
+    t.init_tbs_gpu(batch, max_num_topk=topk, max_num_outpos=steps,
+                   max_num_out_beams=beams, max_num_out_tokens=beams * steps,
+                   max_num_inter_beams=inter)
+    return t
+
+
+@pytest.mark.parametrize("case", KA, ids=[c["name"] for c in KA])
+def test_known_answers(ft, case):
+    print("KA case", case["name"], flush=True)
+    t = _gpu_trie(ft, keys=case["keys"])
+    sents, norms, _, phases = ft.bs_tbs_gpu(
+        t, 1, [case["beams"]], [case["topk_id"]], [case["topk_logp"]],
+        case["token_logp_threshold"], case["sents_logp_threshold"],
+        case["length_norm"], case["early_exit"])
+    assert sents[0] == case["expect_sents"]
+    assert np.allclose(norms[0], case["expect_scores_approx"], rtol=1e-6, atol=0)
+    assert len(phases[0]) == 5
+    s2, n2, _ = ft.tbs(t, case["beams"], case["topk_id"], case["topk_logp"],
+                       case["token_logp_threshold"], case["sents_logp_threshold"],
+                       case["length_norm"], case["early_exit"], True)
+    assert s2 == sents[0] and list(n2) == list(norms[0])
+
+
+def test_known_answers_batched(ft):
+    # KA-5, KA-6, KA-7 share a trie and parameters: one launch
+    cases = [c for c in KA if c["name"].startswith(("KA-5", "KA-6", "KA-7"))]
+    t = _gpu_trie(ft, keys=cases[0]["keys"])
+    sents, norms, _, _ = ft.bs_tbs_gpu(
+        t, len(cases), [c["beams"] for c in cases], [c["topk_id"] for c in cases],
+        [c["topk_logp"] for c in cases], -10.0, -40.0, 0.0, False)
+    for c, s, n in zip(cases, sents, norms):
+        assert s == c["expect_sents"], c["name"]
+        assert np.allclose(n, c["expect_scores_approx"], rtol=1e-6, atol=0)
+
+
+def test_random_tiny_tries(ft, po):
+    rng = np.random.default_rng(7)
+    for case in range(120):
+        vocab = int(rng.integers(2, 10))
+        keys = sorted({tuple(rng.integers(0, vocab, int(rng.integers(1, 7))))
+                       for _ in range(int(rng.integers(1, 40)))})
+        keys = [list(map(int, k)) for k in keys]
+        T = int(rng.integers(1, 8))
+        K = int(rng.integers(1, vocab + 1))
+        B = int(rng.integers(1, 6))
+        ids = np.stack([np.sort(rng.choice(vocab, K, replace=False))
+                        for _ in range(T)]).astype(np.uint32)
+        # quantised logps make exact norm ties common
+        lp = (-rng.integers(0, 8, (T, K)) * 0.5).astype(np.float32)
+        beams = [int(rng.integers(1, B + 1)) for _ in range(T)]
+        early = bool(rng.integers(0, 2))
+        alpha = float(rng.choice([0.0, 1.0, 5.0]))
+        print("tiny case", case, flush=True)
+        t = _gpu_trie(ft, keys=keys, batch=1, topk=16, steps=8, beams=8)
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids.tolist()], [lp.tolist()],
+                            -3.0, -9.0, alpha, early)
+        o = po.OracleTrie.from_keys(keys)
+        want = o.tbs(beams, ids, lp, -3.0, -9.0, alpha, early)
+        assert_same_results((got[0][0], got[1][0]), want, f"tiny case {case}")
+
+
+C1 = dict(n=100000, vocab=32768, lmin=3, lmax=8, s=1.1, seed=0)
+
+
+@pytest.fixture(scope="module")
+def c1(ft, po):
+    toks, offs = ft.synth_keys(C1["n"], C1["vocab"], C1["lmin"], C1["lmax"],
+                               C1["s"], C1["seed"])
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=8, topk=32, steps=8, beams=10,
+                  inter=1024)
+    ids, lp = ft.synth_requests(t, 0, 200, C1["vocab"], 8, 32, 8, 0.3, 2.0,
+                                True, 0)
+    return t, po.OracleTrie.from_keys(toks=toks, offs=offs), ids, lp
+
+
+@pytest.mark.parametrize("early", [False, True])
+def test_c1_batch1(ft, c1, early):
+    t, o, ids, lp = c1
+    beams = [10] * 8
+    nonempty = 0
+    for r in range(200):
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids[r].tolist()], [lp[r].tolist()],
+                            -10.0, -40.0, 5.0, early)
+        want = o.tbs(beams, ids[r], lp[r], -10.0, -40.0, 5.0, early)
+        assert_same_results((got[0][0], got[1][0]), want, f"C1 request {r}")
+        nonempty += len(want[0]) > 0
+    assert nonempty > 150
+
+
+def test_c1_batched_numpy(ft, c1):
+    t, o, ids, lp = c1
+    beams = np.full((8, 8), 10, dtype=np.uint32)
+    for b0 in range(0, 64, 8):
+        ft.stage(t, beams, ids[b0:b0 + 8], lp[b0:b0 + 8], -10.0, -40.0, 5.0, False)
+        ft.launch(t)
+        count, norms, lens, toks, timing = ft.fetch(t)
+        assert timing["kernel_ms"] > 0
+        for i in range(8):
+            want = o.tbs(beams[i], ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, False)
+            n = int(count[i])
+            sents = [toks[i, j, :lens[i, j]].tolist() for j in range(n)]
+            assert_same_results((sents, norms[i, :n]), want, f"batch {b0}+{i}")
+
+
+def test_c1_as_written_oracle(ft, c1, po):
+    t, o, ids, lp = c1
+    for r in range(10):
+        got = ft.tbs(t, [10] * 8, ids[r].tolist(), lp[r].tolist(), -10.0, -40.0,
+                     5.0, False, True)
+        want = o.tbs([10] * 8, ids[r], lp[r], -10.0, -40.0, 5.0, False,
+                     variant=po.AS_WRITTEN)
+        assert_same_results(got[:2], want, f"C1 request {r} (as written)")
+
+
+def test_ties_everywhere(ft, c1):
+    # alpha = 1e6 underflows every length factor beyond depth 1 to 0, so all
+    # norms tie and the arrival-order rule decides every cut
+    t, o, ids, lp = c1
+    for r in range(40):
+        for early in (False, True):
+            got = ft.bs_tbs_gpu(t, 1, [[10] * 8], [ids[r].tolist()],
+                                [lp[r].tolist()], -10.0, -40.0, 1e6, early)
+            want = o.tbs([10] * 8, ids[r], lp[r], -10.0, -40.0, 1e6, early)
+            assert_same_results((got[0][0], got[1][0]), want, f"tie request {r}")
+
+
+def test_unsorted_rows(ft, c1):
+    t, o, ids, lp = c1
+    rng = np.random.default_rng(3)
+    for r in range(30):
+        perm = np.stack([rng.permutation(32) for _ in range(8)])
+        i2 = np.take_along_axis(ids[r], perm, 1)
+        l2 = np.take_along_axis(lp[r], perm, 1)
+        got = ft.bs_tbs_gpu(t, 1, [[6] * 8], [i2.tolist()], [l2.tolist()],
+                            -10.0, -40.0, 5.0, r % 2 == 1)
+        want = o.tbs([6] * 8, i2, l2, -10.0, -40.0, 5.0, r % 2 == 1)
+        assert_same_results((got[0][0], got[1][0]), want, f"unsorted {r}")
+
+
+def test_mixed_beam_widths(ft, c1):
+    t, o, ids, lp = c1
+    rng = np.random.default_rng(5)
+    for r in range(30):
+        beams = [int(x) for x in rng.integers(1, 11, 8)]
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids[r].tolist()], [lp[r].tolist()],
+                            -10.0, -40.0, 5.0, False)
+        want = o.tbs(beams, ids[r], lp[r], -10.0, -40.0, 5.0, False)
+        assert_same_results((got[0][0], got[1][0]), want, f"mixed {r}")
+
+
+def test_request_errors(ft, c1):
+    t, o, ids, lp = c1
+    row = ids[0].tolist()
+    bad = [list(r) for r in row]
+    bad[2][1] = bad[2][0]  # duplicate token id
+    with pytest.raises(RuntimeError, match="duplicate"):
+        ft.bs_tbs_gpu(t, 1, [[10] * 8], [bad], [lp[0].tolist()], -10, -40, 5, False)
+    nan = lp[0].copy()
+    nan[1, 3] = np.nan
+    with pytest.raises(RuntimeError, match="NaN"):
+        ft.bs_tbs_gpu(t, 1, [[10] * 8], [row], [nan.tolist()], -10, -40, 5, False)
+    with pytest.raises(RuntimeError, match="max_num_out_beams"):
+        ft.bs_tbs_gpu(t, 1, [[11] * 8], [row], [lp[0].tolist()], -10, -40, 5, False)
+    with pytest.raises(RuntimeError):
+        ft.bs_tbs_gpu(t, 9, [[10] * 8] * 9, [row] * 9, [lp[0].tolist()] * 9,
+                      -10, -40, 5, False)
+    # final beam 0 leaves the outputs untouched (empty)
+    s, n, _, _ = ft.bs_tbs_gpu(t, 2, [[10] * 7 + [0], [10] * 8], [row, row],
+                               [lp[0].tolist()] * 2, -10, -40, 5, False)
+    assert s[0] == [] and list(n[0]) == []
+    want = o.tbs([10] * 8, ids[0], lp[0], -10, -40, 5, False)
+    assert_same_results((s[1], n[1]), want)
+    # the context still works after errors
+    got = ft.bs_tbs_gpu(t, 1, [[10] * 8], [row], [lp[0].tolist()], -10, -40, 5, False)
+    assert_same_results((got[0][0], got[1][0]), want)
+
+
+def test_history_limit_is_an_error(ft):
+    toks, offs = ft.synth_keys(5000, 256, 3, 6, 1.1, 1)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    t.init_tbs_gpu(1, max_num_topk=32, max_num_outpos=6, max_num_out_beams=10,
+                   max_num_out_tokens=60, max_num_inter_beams=12)
+    ids, lp = ft.synth_requests(t, 0, 1, 256, 6, 32, 8, 0.3, 2.0, True, 0)
+    with pytest.raises(RuntimeError, match="max_num_inter_beams"):
+        ft.bs_tbs_gpu(t, 1, [[10] * 6], [ids[0].tolist()], [lp[0].tolist()],
+                      -10, -40, 5, False)
+
+
+def test_c2_scale_b100(ft, po):
+    # 1M keys over a 256k vocabulary, beam 100, K 100, 12 steps
+    toks, offs = ft.synth_keys(1000000, 262144, 4, 12, 1.1, 1)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=100, steps=12,
+                  beams=100, inter=4096)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 24, 262144, 12, 100, 50, 0.3, 2.0, True, 1)
+    for b0 in range(0, 24, 4):
+        got = ft.bs_tbs_gpu(t, 4, [[100] * 12] * 4,
+                            [ids[b0 + i].tolist() for i in range(4)],
+                            [lp[b0 + i].tolist() for i in range(4)],
+                            -10.0, -40.0, 5.0, False)
+        for i in range(4):
+            want = o.tbs([100] * 12, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0,
+                         False)
+            assert_same_results((got[0][i], got[1][i]), want, f"C2 {b0 + i}")
+
+
+def test_beam_1000(ft, po):
+    toks, offs = ft.synth_keys(1000000, 262144, 3, 10, 1.05, 2)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=2, topk=1000, steps=10,
+                  beams=1000, inter=16384)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 4, 262144, 10, 1000, 1000, 0.3, 2.5, True, 2)
+    for r in range(4):
+        got = ft.bs_tbs_gpu(t, 1, [[1000] * 10], [ids[r].tolist()],
+                            [lp[r].tolist()], -10.0, -40.0, 5.0, False)
+        want = o.tbs([1000] * 10, ids[r], lp[r], -10.0, -40.0, 5.0, False)
+        assert_same_results((got[0][0], got[1][0]), want, f"B1000 {r}")
