@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""Trie beam search benchmark on one MI355X.
+
+A step is one launch of the search kernel over one batch of requests whose
+inputs are already resident in HBM.  Per batch size b in {1, 2, 4, 8} the
+benchmark runs W untimed and K timed launches over a pool of seeded
+synthetic requests, and reports:
+
+  value         peak requests/s over the batch sizes (device-resident)
+  latency_ms    batch-1 kernel latency (HIP events): mean and p99, plus the
+                same through the C++ boundary (host arrays in, results out)
+  roofline      algorithmic bytes per launch / average launch duration,
+                against the 8 TB/s HBM peak
+  cpu_baseline  the CPU oracle (a restatement of the reference's
+                LoudsTrie::tbs) on the host cores, on a bounded sample
+
+Workloads (see --config):
+  paper  synthetic 800M-key trie over a 2.2M-token vocabulary, key length
+         3-16 (mean ~6), Zipf(1.05) prefix sharing; beam = K = 1000, 16 steps
+  c2     10M keys over a 256k vocabulary, length 4-12, Zipf(1.1); beam = K =
+         1000, 12 steps
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config paper]
+"""
+
+import argparse
+import json
+import os
+import sys
+import threading
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-trie_amd"))
+
+METRIC = "mean/p99 trie-search ms @800M keys, beam 1000; peak q/s over batch 1-8"
+HBM_PEAK_GBS = 8000.0
+PUBLISHED_PEAK_QPS = 1539.0  # A100, beam 1000, batch 8 (README.md:64)
+
+TOK_THR, SENT_THR, ALPHA = -10.0, -40.0, 5.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=400,
+                   help="timed launches per batch size")
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default="c2", choices=["c2", "paper"])
+    p.add_argument("--beam", type=int, default=1000)
+    p.add_argument("--pool", type=int, default=512,
+                   help="distinct requests staged in HBM")
+    p.add_argument("--batches", default="1,2,4,8")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--boundary", type=int, default=100,
+                   help="batch-1 requests timed through the C++ boundary")
+    return p.parse_args()
+
+
+def build_workload(ft, cfg, beam):
+    t0 = time.time()
+    if cfg == "c2":
+        vocab, steps = 262144, 12
+        toks, offs = ft.synth_keys(10_000_000, vocab, 4, 12, 1.1, 0)
+        log(f"keys generated in {time.time() - t0:.1f}s")
+        trie = ft.Trie()
+        trie.build_arrays(toks, offs)
+        del toks, offs
+        desc = "10M-key trie, 256k vocab, key length 4-12, Zipf(1.1)"
+    else:
+        vocab, steps = 2_200_000, 16
+        trie = ft.Trie()
+        ft.synth_paper_trie(trie, 800_000_000, vocab, 1.05, 0)
+        desc = ("800M-key trie, 2.2M vocab, key length 3-16 (mean ~6), "
+                "Zipf(1.05) prefix sharing")
+    log(f"trie: {trie.num_keys()} keys, {trie.num_nodes()} nodes, "
+        f"{trie.total_size() / 2**30:.2f} GiB image, {time.time() - t0:.1f}s")
+    return trie, vocab, steps, desc
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the search shards by request "
+              "(replicated trie) with no exchange, see DESIGN.md; "
+              f"--gpus {args.gpus} is not run here", file=sys.stderr)
+        sys.exit(2)
+    import build as ftbuild
+    if not ftbuild.built():
+        ftbuild.build()
+    import flashtrie as ft
+
+    B = K = args.beam
+    trie, vocab, T, desc = build_workload(ft, args.config, B)
+    batches = [int(x) for x in args.batches.split(",")]
+    P = args.pool
+    t0 = time.time()
+    ids, lp = ft.synth_requests(trie, 0, P, vocab, T, K, B, 0.3, 2.5, True, 0,
+                                model=1)
+    beams = np.full((P, T), B, dtype=np.uint32)
+    log(f"{P} requests generated in {time.time() - t0:.1f}s")
+
+    trie.init_tbs_gpu(max(batches), max_num_topk=K, max_num_outpos=T,
+                      max_num_out_beams=B, max_num_out_tokens=B * T,
+                      max_num_inter_beams=B * T)
+    ft.reserve_staging(trie, P)
+    info = trie.device_info()
+    log("device", info)
+    ft.stage(trie, beams, ids, lp, TOK_THR, SENT_THR, ALPHA, False)
+    ft.launch(trie, 0, 1)
+    ft.sync(trie)
+
+    # ---- device-resident throughput and latency per batch size ----------
+    qps, kern_ms, results = {}, {}, {}
+    for b in batches:
+        nb = P // b
+        for i in range(args.warmup):
+            ft.launch(trie, (i % nb) * b, b)
+        ft.sync(trie)
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            ft.launch(trie, (i % nb) * b, b)
+        ft.sync(trie)
+        el = time.perf_counter() - t0
+        n = min(args.steps, 1024)
+        ms = ft.launch_times(trie, n)
+        qps[b] = args.steps * b / el
+        kern_ms[b] = ms
+        log(f"batch {b}: {qps[b]:.0f} q/s, kernel mean {ms.mean():.3f} ms "
+            f"p99 {np.percentile(ms, 99):.3f} ms")
+    peak_b = max(qps, key=qps.get)
+
+    # results + per-phase device time of the whole pool (batches of max b)
+    mb = max(batches)
+    counts, lens_all, phase = [], [], []
+    sample_out = {}
+    for first in range(0, P - P % mb, mb):
+        ft.launch(trie, first, mb)
+    ft.sync(trie)
+    cnt, norms, lens, toks, timing = ft.fetch(trie)
+    used = P - P % mb
+    counts = cnt[:used]
+    dev = timing["device_ms"][:used]
+    phase = {"expand_ms": float(dev[:, 0].mean()),
+             "select_ms": float(dev[:, 1].mean()),
+             "other_ms": float(dev[:, 2].mean()),
+             "device_total_ms": float(dev[:, 3].mean())}
+
+    # ---- batch-1 latency through the C++ boundary (host arrays) -----------
+    bl = []
+    nbd = min(args.boundary, P)
+    for r in range(nbd):
+        t0 = time.perf_counter()
+        ft.stage(trie, beams[r:r + 1], ids[r:r + 1], lp[r:r + 1], TOK_THR,
+                 SENT_THR, ALPHA, False)
+        ft.launch(trie)
+        c1, n1, l1, t1, _ = ft.fetch(trie)
+        bl.append((time.perf_counter() - t0) * 1e3)
+    bl = np.array(bl)
+
+    # ---- CPU oracle baseline on a bounded sample + parity spot check -------
+    cpu = None
+    parity = {"checked": 0, "mismatches": 0}
+    algo_bytes = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle
+        img = trie.image()
+        hdr = np.frombuffer(img[:64].tobytes(), dtype="<u8", count=8)
+        nn, ro, to, tl = int(hdr[1]), int(hdr[4]), int(hdr[6]), int(hdr[3])
+        recs = img[ro:ro + (nn + 1) * 16]
+        tail = img[to:to + max(tl, 1) * 4].view(np.uint32)
+        ot = pyoracle.OracleTrie.from_image(recs, tail, nn)
+        cores = min(os.cpu_count() or 1, 16)
+        done, works, lock = [], [], threading.Lock()
+        deadline = time.time() + args.cpu_seconds
+        nxt = [0]
+
+        def worker():
+            while time.time() < deadline:
+                with lock:
+                    r = nxt[0]
+                    nxt[0] += 1
+                if r >= P:
+                    return
+                s, n, w = ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR,
+                                 ALPHA, False, with_work=True)
+                with lock:
+                    done.append((r, s, n))
+                    works.append(w)
+
+        t0 = time.time()
+        th = [threading.Thread(target=worker) for _ in range(cores)]
+        [x.start() for x in th]
+        [x.join() for x in th]
+        cpu_el = time.time() - t0
+        # single-thread latency of the same restatement, and the as-written
+        # cost model (thread per parent, linear sibling scan) on 2 requests
+        lat1 = []
+        for r in range(3):
+            t1 = time.perf_counter()
+            ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, False)
+            lat1.append((time.perf_counter() - t1) * 1e3)
+        aw = []
+        for r in range(2):
+            t1 = time.perf_counter()
+            ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, False,
+                   variant=pyoracle.AS_WRITTEN)
+            aw.append((time.perf_counter() - t1) * 1e3)
+        cpu = {"value": len(done) / cpu_el, "unit": "q/s", "cores": cores,
+               "kind": "port",
+               "sample": f"{len(done)} of the {P} pooled requests in "
+                         f"{cpu_el:.1f}s on {cores} threads (oracle, binary "
+                         f"sibling search); 1-thread latency "
+                         f"{np.mean(lat1):.1f} ms; as-written cost model "
+                         f"(thread per parent, linear sibling scan) "
+                         f"{np.mean(aw):.1f} ms/request"}
+        # parity of the GPU results for the sampled requests
+        for r, s, n in done:
+            if r >= used:
+                continue
+            c = int(counts[r])
+            g = [toks[r, j, :lens[r, j]].tolist() for j in range(c)]
+            parity["checked"] += 1
+            if g != s or not np.array_equal(norms[r, :c], n):
+                parity["mismatches"] += 1
+        # algorithmic bytes per request (work counters of the oracle):
+        # 8K per row + 16 per parent + 16 per non-link parent + 4 per child
+        # label touched + 32 per candidate + 16 per survivor + result bytes
+        W = np.array(works, dtype=np.float64)
+        res_b = np.array([16 + 16 * len(s) + 4 * sum(map(len, s))
+                          for _, s, _ in done], dtype=np.float64)
+        per_req = (W[:, 6] + 16 * W[:, 1] + 16 * (W[:, 1] - W[:, 2]) +
+                   4 * W[:, 3] + 32 * W[:, 4] + 16 * W[:, 5] + res_b)
+        algo_bytes = float(per_req.mean())
+        wstats = {"steps": float(W[:, 0].mean()), "parents": float(W[:, 1].mean()),
+                  "link_parents": float(W[:, 2].mean()),
+                  "candidates": float(W[:, 4].mean()),
+                  "results": float(np.mean([len(s) for _, s, _ in done]))}
+    else:
+        wstats = {}
+
+    kb = kern_ms[peak_b]
+    roof = None
+    if algo_bytes is not None:
+        achieved = algo_bytes * peak_b / (kb.mean() * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 3),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "algorithmic_bytes_per_request": round(algo_bytes),
+                "requests_per_launch": peak_b}
+    k1 = kern_ms.get(1, kb)
+    out = {
+        "metric": METRIC,
+        "value": round(qps[peak_b], 1),
+        "unit": "q/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(float(kb.mean()), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": (round(qps[peak_b] / PUBLISHED_PEAK_QPS, 3)
+                        if args.config == "paper" else None),
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": desc, "beam": B, "topk": K, "steps": T,
+                   "batch_sizes": batches, "peak_batch": peak_b,
+                   "requests_pooled": P,
+                   "proposals": "example row model: seed-path tokens "
+                                "U(-2.2,-0.2), distractors U(-12,-4), "
+                                f"{B} seed paths",
+                   "thresholds": [TOK_THR, SENT_THR], "length_norm": ALPHA},
+        "latency_ms": {"mean": round(float(k1.mean()), 4),
+                       "p99": round(float(np.percentile(k1, 99)), 4),
+                       "boundary_mean": round(float(bl.mean()), 4),
+                       "boundary_p99": round(float(np.percentile(bl, 99)), 4)},
+        "qps_by_batch": {str(b): round(v, 1) for b, v in qps.items()},
+        "kernel_ms_by_batch": {str(b): round(float(v.mean()), 4)
+                               for b, v in kern_ms.items()},
+        "phases_ms_per_request": phase,
+        "workload_stats": wstats,
+        "parity": parity,
+        "device": info,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

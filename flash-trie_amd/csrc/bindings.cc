@@ -304,7 +304,31 @@ PYBIND11_MODULE(flashtrie, m) {
       py::arg("trie"), py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"),
       py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
       py::arg("length_norm"), py::arg("early_exit"));
-  m.def("launch", [](Trie& trie) { check_ft(ft_launch(ctx_of(trie)), "launch"); });
+  m.def(
+      "launch",
+      [](Trie& trie, size_t first, size_t count) {
+        ft_ctx* c = ctx_of(trie);
+        if (count == 0) check_ft(ft_launch(c), "launch");
+        else check_ft(ft_launch_range(c, first, count), "launch");
+      },
+      py::arg("trie"), py::arg("first") = 0, py::arg("count") = 0);
+  m.def(
+      "reserve_staging",
+      [](Trie& trie, size_t n) { check_ft(ft_reserve_staging(ctx_of(trie), n), "reserve_staging"); },
+      py::arg("trie"), py::arg("max_staged"));
+  m.def(
+      "launch_times",
+      [](Trie& trie, size_t n) {
+        py::array_t<double> ms((py::ssize_t)n);
+        int rc;
+        {
+          py::gil_scoped_release nogil;
+          rc = ft_launch_times(ctx_of(trie), ms.mutable_data(), n);
+        }
+        check_ft(rc, "launch_times");
+        return ms;
+      },
+      py::arg("trie"), py::arg("n"));
   m.def("sync", [](Trie& trie) {
     double ms = 0.0;
     {
@@ -386,7 +410,7 @@ PYBIND11_MODULE(flashtrie, m) {
       "synth_requests",
       [](const Trie& trie, uint64_t first, uint64_t count, uint32_t vocab, uint32_t steps,
          uint32_t topk, uint32_t seed_paths, double seed_mass, double sigma,
-         bool analytic_rest, uint64_t seed, int threads) {
+         bool analytic_rest, uint64_t seed, int threads, int model) {
         const ftamd::ImageBlob& img = image_of(trie);
         ftamd::synth::ProposalSpec sp;
         sp.vocab = vocab;
@@ -396,6 +420,8 @@ PYBIND11_MODULE(flashtrie, m) {
         sp.seed_mass = seed_mass;
         sp.sigma = sigma;
         sp.analytic_rest = analytic_rest;
+        sp.model = model == 1 ? ftamd::synth::ProposalSpec::kExample
+                              : ftamd::synth::ProposalSpec::kSoftmax;
         py::array_t<uint32_t> ids({(py::ssize_t)count, (py::ssize_t)steps, (py::ssize_t)topk});
         py::array_t<float> lp({(py::ssize_t)count, (py::ssize_t)steps, (py::ssize_t)topk});
         uint32_t* ip = ids.mutable_data();
@@ -421,5 +447,6 @@ PYBIND11_MODULE(flashtrie, m) {
       },
       py::arg("trie"), py::arg("first"), py::arg("count"), py::arg("vocab"),
       py::arg("steps"), py::arg("topk"), py::arg("seed_paths"), py::arg("seed_mass"),
-      py::arg("sigma"), py::arg("analytic_rest"), py::arg("seed"), py::arg("threads") = 0);
+      py::arg("sigma"), py::arg("analytic_rest"), py::arg("seed"), py::arg("threads") = 0,
+      py::arg("model") = 0);
 }

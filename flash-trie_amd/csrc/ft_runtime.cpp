@@ -50,7 +50,6 @@ struct ft_ctx {
   uint8_t* d_image = nullptr;
   ft_image_header hdr{};
   hipStream_t stream = nullptr;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
   int num_cus = 0, lds_per_block = 0, wall_khz = 0;
   char name[64] = {0};
 
@@ -67,10 +66,17 @@ struct ft_ctx {
   uint8_t* d_stage = nullptr;
   uint8_t* h_stage = nullptr;
 
+  size_t max_staged = 0;  // staging / output capacity in requests
+  uint64_t per_req = 0;   // staging bytes bound of one request
+
   std::vector<StagedReq> staged;
   uint64_t out_stride = 0;
   bool launched = false;
   uint32_t scan_mult = 8;
+  // ring of (start, end) event pairs, one pair per launch
+  static constexpr size_t kRing = 1024;
+  std::vector<hipEvent_t> ring;
+  uint64_t launches = 0;
 };
 
 static void release_workspace(ft_ctx* c) {
@@ -81,6 +87,28 @@ static void release_workspace(ft_ctx* c) {
   if (c->h_stage) (void)hipHostFree(c->h_stage);
   c->d_ws = c->d_out = c->d_stage = c->h_out = c->h_stage = nullptr;
   c->reserved = false;
+}
+
+// (Re)allocates the staging and output buffers for n requests.
+static int alloc_staging(ft_ctx* c, size_t n) {
+  if (c->d_out) (void)hipFree(c->d_out);
+  if (c->d_stage) (void)hipFree(c->d_stage);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->h_stage) (void)hipHostFree(c->h_stage);
+  c->d_out = c->d_stage = c->h_out = c->h_stage = nullptr;
+  c->max_staged = 0;
+  c->stage_cap = align_up(n * sizeof(DevReq), 256) + n * c->per_req;
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_out, c->out_slot_max * n)) != hipSuccess)
+    return hip_fail(e, "hipMalloc(output)");
+  if ((e = hipMalloc(&c->d_stage, c->stage_cap)) != hipSuccess)
+    return hip_fail(e, "hipMalloc(stage)");
+  if ((e = hipHostMalloc(&c->h_out, c->out_slot_max * n, 0)) != hipSuccess)
+    return hip_fail(e, "hipHostMalloc(output)");
+  if ((e = hipHostMalloc(&c->h_stage, c->stage_cap, 0)) != hipSuccess)
+    return hip_fail(e, "hipHostMalloc(stage)");
+  c->max_staged = n;
+  return FT_OK;
 }
 
 extern "C" {
@@ -158,8 +186,8 @@ int ft_create(const void* image, size_t image_bytes, int device,
     delete c;
     return hip_fail(e, "hipStreamCreate");
   }
-  (void)hipEventCreate(&c->ev0);
-  (void)hipEventCreate(&c->ev1);
+  c->ring.assign(2 * ft_ctx::kRing, nullptr);
+  for (auto& ev : c->ring) (void)hipEventCreate(&ev);
   if (const char* s = std::getenv("FT_SCAN_MULT")) {
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
@@ -207,22 +235,13 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   c->ws_stride = off;
   c->out_slot_max = align_up(sizeof(OutHeader) + 12 * B + 4 * (uint64_t)max_out_tokens, 256);
   // per request: lnf + beams + ids + logps + row flags + permutation
-  const uint64_t per_req = align_up(8 * (max_steps + 1), 16) +
-                           align_up(4 * max_steps, 16) +
-                           3 * align_up(4 * max_steps * K, 16) +
-                           align_up(max_steps, 16) + 256;
-  c->stage_cap = align_up(max_batch * sizeof(DevReq), 256) + max_batch * per_req;
+  c->per_req = align_up(8 * (max_steps + 1), 16) + align_up(4 * max_steps, 16) +
+               3 * align_up(4 * max_steps * K, 16) + align_up(max_steps, 16) + 256;
   hipError_t e;
   if ((e = hipMalloc(&c->d_ws, c->ws_stride * max_batch)) != hipSuccess)
     return release_workspace(c), hip_fail(e, "hipMalloc(workspace)");
-  if ((e = hipMalloc(&c->d_out, c->out_slot_max * max_batch)) != hipSuccess)
-    return release_workspace(c), hip_fail(e, "hipMalloc(output)");
-  if ((e = hipMalloc(&c->d_stage, c->stage_cap)) != hipSuccess)
-    return release_workspace(c), hip_fail(e, "hipMalloc(stage)");
-  if ((e = hipHostMalloc(&c->h_out, c->out_slot_max * max_batch, 0)) != hipSuccess)
-    return release_workspace(c), hip_fail(e, "hipHostMalloc(output)");
-  if ((e = hipHostMalloc(&c->h_stage, c->stage_cap, 0)) != hipSuccess)
-    return release_workspace(c), hip_fail(e, "hipHostMalloc(stage)");
+  int rc = alloc_staging(c, max_batch);
+  if (rc) return release_workspace(c), rc;
   c->max_batch = max_batch;
   c->max_topk = max_topk;
   c->max_steps = max_steps;
@@ -238,10 +257,9 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
 int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
   if (!c || (!reqs && batch)) return fail(FT_E_ARG, "ft_stage: null argument");
   if (!c->reserved) return fail(FT_E_STATE, "ft_stage: init_tbs_gpu (ft_reserve) was not called");
-  if (batch == 0 || batch > c->max_batch)
+  if (batch == 0 || batch > c->max_staged)
     return fail(FT_E_LIMIT, "ft_stage: batch size " + std::to_string(batch) +
-                                " not in [1, max_batch_size=" +
-                                std::to_string(c->max_batch) + "]");
+                                " not in [1, " + std::to_string(c->max_staged) + "]");
   c->staged.assign(batch, StagedReq());
   c->launched = false;
   uint8_t* H = c->h_stage;
@@ -301,9 +319,10 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     uint64_t o = 0;
     // length-norm table, exactly Agent::logp_norm's factor (agent.h:69-72)
     double* lnf = (double*)(base + o);
+    // (depth 0 is the root alone, whose norm is never compared)
     for (uint32_t dd = 0; dd <= T; ++dd) {
       lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
-      if (!std::isfinite(lnf[dd]))
+      if (dd > 0 && !std::isfinite(lnf[dd]))
         return fail(FT_E_INPUT, who + "length_norm gives a non-finite factor");
     }
     o = align_up(o + 8ull * (T + 1), 16);
@@ -374,30 +393,70 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
 
 int ft_launch(ft_ctx* c) {
   if (!c) return fail(FT_E_ARG, "ft_launch: null context");
+  return ft_launch_range(c, 0, c->staged.size());
+}
+
+int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
+  if (!c) return fail(FT_E_ARG, "ft_launch_range: null context");
   if (c->staged.empty()) return fail(FT_E_STATE, "ft_launch: nothing staged");
+  if (count == 0 || count > c->max_batch || first + count > c->staged.size())
+    return fail(FT_E_LIMIT, "ft_launch_range: [" + std::to_string(first) + ", +" +
+                                std::to_string(count) + ") exceeds the staged requests or max_batch_size " +
+                                std::to_string(c->max_batch));
   KArgs a{};
   a.recs = (const ft_node_rec*)(c->d_image + c->hdr.recs_offset);
   a.parent = (const uint32_t*)(c->d_image + c->hdr.parent_offset);
   a.tail = (const uint32_t*)(c->d_image + c->hdr.tail_offset);
-  a.reqs = (const DevReq*)c->d_stage;
+  a.reqs = (const DevReq*)c->d_stage + first;
   a.stage = c->d_stage;
   a.ws = c->d_ws;
   a.ws_stride = c->ws_stride;
-  a.out = c->d_out;
+  a.out = c->d_out + first * c->out_stride;
   a.out_stride = c->out_stride;
   a.lay = c->lay;
-  a.batch = (uint32_t)c->staged.size();
+  a.batch = (uint32_t)count;
   uint32_t kmax = 1;
-  for (auto& s : c->staged) kmax = std::max(kmax, s.K);
+  for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
   const uint64_t sl = (uint64_t)c->scan_mult * kmax;
   a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
   (void)hipSetDevice(c->device);
-  (void)hipEventRecord(c->ev0, c->stream);
+  const size_t slot = (c->launches % ft_ctx::kRing) * 2;
+  (void)hipEventRecord(c->ring[slot], c->stream);
   hipError_t e = launch_tbs(a, c->stream);
   if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel");
-  (void)hipEventRecord(c->ev1, c->stream);
+  (void)hipEventRecord(c->ring[slot + 1], c->stream);
+  ++c->launches;
   c->launched = true;
   return FT_OK;
+}
+
+int ft_launch_times(ft_ctx* c, double* ms, size_t n) {
+  if (!c || (!ms && n)) return fail(FT_E_ARG, "ft_launch_times: null argument");
+  if (n > c->launches || n > ft_ctx::kRing)
+    return fail(FT_E_ARG, "ft_launch_times: fewer launches recorded");
+  (void)hipSetDevice(c->device);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+  for (size_t i = 0; i < n; ++i) {
+    const uint64_t L = c->launches - n + i;
+    const size_t slot = (L % ft_ctx::kRing) * 2;
+    float f = 0.f;
+    e = hipEventElapsedTime(&f, c->ring[slot], c->ring[slot + 1]);
+    if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+    ms[i] = f;
+  }
+  return FT_OK;
+}
+
+int ft_reserve_staging(ft_ctx* c, size_t max_staged) {
+  if (!c) return fail(FT_E_ARG, "ft_reserve_staging: null context");
+  if (!c->reserved) return fail(FT_E_STATE, "ft_reserve_staging: ft_reserve was not called");
+  if (max_staged < c->max_batch) max_staged = c->max_batch;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  c->staged.clear();
+  c->launched = false;
+  return alloc_staging(c, max_staged);
 }
 
 int ft_sync(ft_ctx* c, double* ms) {
@@ -407,7 +466,10 @@ int ft_sync(ft_ctx* c, double* ms) {
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
   if (ms) {
     float f = 0.f;
-    (void)hipEventElapsedTime(&f, c->ev0, c->ev1);
+    if (c->launches) {
+      const size_t slot = ((c->launches - 1) % ft_ctx::kRing) * 2;
+      (void)hipEventElapsedTime(&f, c->ring[slot], c->ring[slot + 1]);
+    }
     *ms = f;
   }
   return FT_OK;
@@ -503,8 +565,8 @@ void ft_destroy(ft_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   release_workspace(c);
   if (c->d_image) (void)hipFree(c->d_image);
-  if (c->ev0) (void)hipEventDestroy(c->ev0);
-  if (c->ev1) (void)hipEventDestroy(c->ev1);
+  for (auto& ev : c->ring)
+    if (ev) (void)hipEventDestroy(ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }

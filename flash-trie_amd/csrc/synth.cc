@@ -206,6 +206,24 @@ void make_request(const ImageBlob& img, const ProposalSpec& sp,
       if (std::find(dis.begin(), dis.end(), tok) != dis.end()) continue;
       dis.push_back(tok);
     }
+    if (sp.model == ProposalSpec::kExample) {
+      cell.clear();
+      for (size_t i = 0; i < m; ++i)
+        cell.push_back({row[i], (float)(-0.2 - 2.0 * r.uniform())});
+      for (size_t i = 0; i < dis.size(); ++i)
+        cell.push_back({dis[i], (float)(-4.0 - 8.0 * r.uniform())});
+      std::sort(cell.begin(), cell.end());
+      for (uint32_t k = 0; k < K; ++k) {
+        if (k < cell.size()) {
+          ids[(uint64_t)t * K + k] = cell[k].first;
+          logp[(uint64_t)t * K + k] = cell[k].second;
+        } else {
+          ids[(uint64_t)t * K + k] = sp.vocab + k;
+          logp[(uint64_t)t * K + k] = -INFINITY;
+        }
+      }
+      continue;
+    }
     zseed.assign(m, 0.0);
     for (size_t i = 0; i < m; ++i) zseed[i] = sp.sigma * r.normal();
     zother.assign(dis.size(), 0.0);

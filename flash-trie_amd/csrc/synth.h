@@ -72,6 +72,11 @@ struct ProposalSpec {
   double seed_mass = 0.3;   // softmax mass carried by the forced tokens
   double sigma = 2.0;       // logits ~ N(0, sigma^2)
   bool analytic_rest = false;  // include the unproposed vocabulary in logZ
+  // Row model.  kSoftmax: log-softmax of N(0, sigma^2) logits with
+  // seed_mass of the mass on the forced tokens.  kExample: the shape of the
+  // reference's example generator (examples/make_example_data.py:119-145):
+  // forced tokens uniform in [-2.2, -0.2], distractors uniform in [-12, -4].
+  enum Model { kSoftmax = 0, kExample = 1 } model = kSoftmax;
 };
 
 // Proposal rows of one request, sorted by token id: ids[T*K], logp[T*K].

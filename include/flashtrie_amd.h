@@ -153,8 +153,22 @@ int ft_reserve(ft_ctx* ctx, size_t max_batch, size_t max_topk,
  * the device workspace (async on the context stream). */
 int ft_stage(ft_ctx* ctx, const ft_request* reqs, size_t batch);
 
-/* Launches the search kernel over the staged batch (async). */
+/* Launches the search kernel over the staged batch (async); at most
+ * max_batch requests. */
 int ft_launch(ft_ctx* ctx);
+
+/* Grows the staging and result buffers to hold `max_staged` requests, so a
+ * larger set can be staged once and searched in ranges (device-resident
+ * inputs).  Workspace slots stay at max_batch. */
+int ft_reserve_staging(ft_ctx* ctx, size_t max_staged);
+
+/* Launches the staged requests [first, first + count), count <= max_batch
+ * (async). */
+int ft_launch_range(ft_ctx* ctx, size_t first, size_t count);
+
+/* Kernel durations (HIP events) of the last n launches, oldest first;
+ * waits for the stream.  At most 1024 are kept. */
+int ft_launch_times(ft_ctx* ctx, double* ms, size_t n);
 
 /* Waits for the last launch, copies results back, fills `results`. */
 int ft_fetch(ft_ctx* ctx, ft_result* results, size_t batch,
