@@ -52,7 +52,7 @@ def parse():
     p.add_argument("--steps", type=int, default=400,
                    help="timed launches per batch size")
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", default="c2", choices=["c2", "paper"])
+    p.add_argument("--config", default="paper", choices=["c2", "paper"])
     p.add_argument("--beam", type=int, default=1000)
     p.add_argument("--pool", type=int, default=512,
                    help="distinct requests staged in HBM")
@@ -77,6 +77,7 @@ def build_workload(ft, cfg, beam):
     else:
         vocab, steps = 2_200_000, 16
         trie = ft.Trie()
+        os.environ["FT_SYNTH_VERBOSE"] = "1"  # per-level progress on stderr
         ft.synth_paper_trie(trie, 800_000_000, vocab, 1.05, 0)
         desc = ("800M-key trie, 2.2M vocab, key length 3-16 (mean ~6), "
                 "Zipf(1.05) prefix sharing")
@@ -172,7 +173,7 @@ def main():
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import pyoracle
-        img = trie.image()
+        img = trie.image_view()
         hdr = np.frombuffer(img[:64].tobytes(), dtype="<u8", count=8)
         nn, ro, to, tl = int(hdr[1]), int(hdr[4]), int(hdr[6]), int(hdr[3])
         recs = img[ro:ro + (nn + 1) * 16]

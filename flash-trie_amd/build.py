@@ -69,6 +69,7 @@ def build(verbose=False):
         "marisa_trie.cc": os.path.join(OBJ, "marisa_trie.o"),
         "image_builder.cc": os.path.join(OBJ, "image_builder.o"),
         "synth.cc": os.path.join(OBJ, "synth.o"),
+        "synth_trie.cc": os.path.join(OBJ, "synth_trie.o"),
     }
     bind_obj = os.path.join(OBJ, "bindings.o")
     jobs = []

@@ -183,6 +183,14 @@ PYBIND11_MODULE(flashtrie, m) {
              const ftamd::ImageBlob& img = image_of(t);
              return py::array_t<uint8_t>((py::ssize_t)img.size(), img.data());
            })
+      .def("image_view",
+           [](py::object self) {
+             // zero-copy view of the image; keeps the Trie alive
+             const Trie& t = self.cast<const Trie&>();
+             const ftamd::ImageBlob& img = image_of(t);
+             return py::array_t<uint8_t>({(py::ssize_t)img.size()}, {(py::ssize_t)1},
+                                         img.data(), self);
+           })
       .def("assign_image",
            [](Trie& t, py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a) {
              t.assign_image(a.data(), (size_t)a.size());
@@ -406,6 +414,38 @@ PYBIND11_MODULE(flashtrie, m) {
       },
       py::arg("n"), py::arg("vocab"), py::arg("lmin"), py::arg("lmax"), py::arg("s"),
       py::arg("seed"));
+  m.def(
+      "synth_paper_trie",
+      [](Trie& trie, uint64_t n_keys, uint32_t vocab, double s, uint64_t seed,
+         uint32_t lmin, uint32_t lmax, double p_end, int threads) {
+        ftamd::ImageBlob img;
+        std::string err;
+        bool ok;
+        {
+          py::gil_scoped_release nogil;
+          ok = ftamd::synth::make_paper_trie(n_keys, vocab, s, lmin, lmax, p_end,
+                                             seed, threads, &img, &err);
+        }
+        if (!ok) throw marisa::Exception(MARISA_SIZE_ERROR, "synth_paper_trie: " + err);
+        marisa::TrieImpl* im = trie.impl();
+        im->drop_gpu();
+        im->img.swap(img);
+      },
+      py::arg("trie"), py::arg("n_keys"), py::arg("vocab"), py::arg("s"),
+      py::arg("seed"), py::arg("lmin") = 3, py::arg("lmax") = 16,
+      py::arg("p_end") = 0.25, py::arg("threads") = 0);
+  m.def(
+      "validate_image",
+      [](const Trie& trie) {
+        std::string err;
+        bool ok;
+        {
+          py::gil_scoped_release nogil;
+          ok = ftamd::validate_image(image_of(trie), &err);
+        }
+        if (!ok) throw marisa::Exception(MARISA_FORMAT_ERROR, "validate_image: " + err);
+      },
+      py::arg("trie"));
   m.def(
       "synth_requests",
       [](const Trie& trie, uint64_t first, uint64_t count, uint32_t vocab, uint32_t steps,

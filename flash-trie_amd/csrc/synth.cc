@@ -162,23 +162,42 @@ void make_request(const ImageBlob& img, const ProposalSpec& sp,
                   float* logp) {
   const uint32_t T = sp.steps, K = sp.topk;
   const ft_node_rec* R = img.recs();
-  // seed paths through the search state machine
+  // Seed paths: uniformly random keys (like the reference's example
+  // generator, examples/make_example_data.py:153-154), each replayed through
+  // the search state machine along its node path -- the pending key token
+  // at a terminal link node, else the next node of the path -- so every
+  // forced token is a valid continuation at its step.
+  const uint64_t N = img.header().num_nodes;
   std::vector<std::vector<uint32_t>> paths(sp.seed_paths);
+  std::vector<uint32_t> chain;
   for (uint32_t sidx = 0; sidx < sp.seed_paths; ++sidx) {
     Rng r(seed ^ 0x5EEDull, request * 1000003ull + sidx);
+    if (img.header().num_keys == 0 || N < 2) break;
+    uint32_t target = 0;
+    for (int tries = 0; tries < 4096; ++tries) {
+      const uint32_t v = 1 + (uint32_t)r.below(N - 1);
+      if (R[v].meta & FT_META_TERMINAL) {
+        target = v;
+        break;
+      }
+    }
+    if (!target) continue;
+    chain.clear();
+    for (uint32_t v = target; v != 0; v = img.parent()[v]) chain.push_back(v);
     uint32_t node = 0;
+    size_t next = chain.size();  // chain is target..first; walk backwards
     for (uint32_t t = 0; t < T; ++t) {
       const uint32_t m = R[node].meta;
       uint32_t tok;
       if ((m & FT_META_TERMINAL) && (m & FT_META_DEPTH_MASK) > t) {
         tok = kb_token(img, node, t);
       } else {
-        const uint32_t c0 = R[node].child_begin, c1 = R[node + 1].child_begin;
-        if (c0 == c1) break;
-        node = c0 + (uint32_t)r.below(c1 - c0);
+        if (next == 0) break;
+        node = chain[--next];
         tok = R[node].first_tok;
       }
       paths[sidx].push_back(tok);
+      if (node == target && (m & FT_META_DEPTH_MASK) == t + 1) break;
     }
   }
   std::vector<uint32_t> row;

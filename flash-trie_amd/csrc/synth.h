@@ -6,6 +6,7 @@
 #pragma once
 
 #include <cstdint>
+#include <string>
 #include <vector>
 
 #include "image_builder.h"
@@ -86,6 +87,14 @@ struct ProposalSpec {
 void make_request(const ImageBlob& img, const ProposalSpec& spec,
                   uint64_t seed, uint64_t request, uint32_t* ids,
                   float* logp);
+
+// Paper-scale trie generated level by level without materialising keys:
+// n_keys independent keys (duplicates dropped), length lmin + Geometric(p_end)
+// truncated at lmax, Zipf(zipf_s) tokens over a prefix-keyed permutation of
+// the vocabulary.  Writes the image directly (reference node numbering).
+bool make_paper_trie(uint64_t n_keys, uint32_t vocab, double zipf_s,
+                     uint32_t lmin, uint32_t lmax, double p_end, uint64_t seed,
+                     int threads, ImageBlob* out, std::string* err);
 
 }  // namespace synth
 }  // namespace ftamd
