@@ -360,6 +360,8 @@ PYBIND11_MODULE(flashtrie, m) {
     py::array_t<uint32_t> lens({(py::ssize_t)B, (py::ssize_t)Fm});
     py::array_t<uint32_t> toks({(py::ssize_t)B, (py::ssize_t)Fm, (py::ssize_t)Tm});
     py::array_t<double> dev({(py::ssize_t)B, (py::ssize_t)4});
+    py::array_t<uint64_t> steps({(py::ssize_t)B, (py::ssize_t)Tm, (py::ssize_t)8});
+    std::memset(steps.mutable_data(), 0, B * Tm * 8 * 8);
     std::memset(norms.mutable_data(), 0, B * Fm * 8);
     std::memset(lens.mutable_data(), 0, B * Fm * 4);
     std::memset(toks.mutable_data(), 0, B * Fm * Tm * 4);
@@ -371,6 +373,7 @@ PYBIND11_MODULE(flashtrie, m) {
       res[b].logp_norm = norms.mutable_data() + b * Fm;
       res[b].length = lens.mutable_data() + b * Fm;
       res[b].tokens = toks.mutable_data() + b * Fm * Tm;
+      res[b].step_stats = steps.mutable_data() + b * Tm * 8;
     }
     ft_timing tm{};
     int rc;
@@ -393,6 +396,7 @@ PYBIND11_MODULE(flashtrie, m) {
     d["children"] = tm.children;
     d["probes"] = tm.probes;
     d["device_ms"] = dev;
+    d["step_stats"] = steps;
     return py::make_tuple(count, norms, lens, toks, d);
   });
 

@@ -9,7 +9,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <thread>
 #include <cstdio>
 #include <cstring>
 #include <limits>
@@ -69,6 +71,12 @@ struct ft_ctx {
   size_t max_staged = 0;  // staging / output capacity in requests
   uint64_t per_req = 0;   // staging bytes bound of one request
 
+  // wide-node index (device)
+  WideDir* d_wdir = nullptr;
+  WideSlot* d_wtab = nullptr;
+  uint32_t wdir_log2 = 0, wide_min = 0;
+  uint64_t wide_nodes = 0, wide_slots = 0;
+
   std::vector<StagedReq> staged;
   uint64_t out_stride = 0;
   bool launched = false;
@@ -108,6 +116,87 @@ static int alloc_staging(ft_ctx* c, size_t n) {
   if ((e = hipHostMalloc(&c->h_stage, c->stage_cap, 0)) != hipSuccess)
     return hip_fail(e, "hipHostMalloc(stage)");
   c->max_staged = n;
+  return FT_OK;
+}
+
+// Builds the wide-node index on the host (parallel) and uploads it.
+static int build_wide_index(ft_ctx* c, const uint8_t* image) {
+  const char* env = std::getenv("FT_WIDE_MIN");
+  long wmin = env ? std::strtol(env, nullptr, 10) : 512;
+  if (wmin <= 0) return FT_OK;  // disabled
+  const uint64_t N = c->hdr.num_nodes;
+  const ft_node_rec* R = (const ft_node_rec*)(image + c->hdr.recs_offset);
+  const int T = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::vector<uint32_t>> found(T);
+  {
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&, w]() {
+        const uint64_t b = N * w / T, e = N * (w + 1) / T;
+        for (uint64_t n = b; n < e; ++n)
+          if (R[n + 1].child_begin - R[n].child_begin >= (uint32_t)wmin)
+            found[w].push_back((uint32_t)n);
+      });
+    for (auto& x : th) x.join();
+  }
+  std::vector<uint32_t> nodes;
+  for (auto& f : found) nodes.insert(nodes.end(), f.begin(), f.end());
+  if (nodes.empty()) return FT_OK;
+  std::vector<WideDir> ent(nodes.size());
+  uint64_t slots = 0;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const uint32_t n = nodes[i];
+    const uint64_t deg = R[n + 1].child_begin - R[n].child_begin;
+    uint32_t lg = 1;
+    while ((1ull << lg) < 2 * deg) ++lg;
+    ent[i] = WideDir{n, lg, (uint32_t)slots, 0};
+    slots += 1ull << lg;
+  }
+  if (slots >= 0xFFFFFFF0ull) return fail(FT_E_IMAGE, "wide-node index too large");
+  uint32_t dlg = 1;
+  while ((1ull << dlg) < 2 * nodes.size()) ++dlg;
+  std::vector<WideDir> dir(1ull << dlg, WideDir{kEmpty, 0, 0, 0});
+  for (const WideDir& e : ent) {
+    uint32_t sl = fib_slot(e.node, dlg);
+    while (dir[sl].node != kEmpty) sl = (sl + 1) & ((1u << dlg) - 1);
+    dir[sl] = e;
+  }
+  std::vector<WideSlot> tab(slots, WideSlot{kEmpty, 0});
+  {
+    std::atomic<size_t> next{0};
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&]() {
+        for (;;) {
+          const size_t i = next.fetch_add(1);
+          if (i >= ent.size()) break;
+          const WideDir& e = ent[i];
+          WideSlot* t = tab.data() + e.slot_off;
+          const uint32_t mask = (1u << e.log2size) - 1;
+          for (uint32_t ch = R[e.node].child_begin; ch < R[e.node + 1].child_begin; ++ch) {
+            uint32_t sl = fib_slot(R[ch].first_tok, e.log2size);
+            while (t[sl].tok != kEmpty) sl = (sl + 1) & mask;
+            t[sl] = WideSlot{R[ch].first_tok, ch};
+          }
+        }
+      });
+    for (auto& x : th) x.join();
+  }
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_wdir, dir.size() * sizeof(WideDir))) != hipSuccess)
+    return hip_fail(e, "hipMalloc(wide dir)");
+  if ((e = hipMalloc(&c->d_wtab, tab.size() * sizeof(WideSlot))) != hipSuccess)
+    return hip_fail(e, "hipMalloc(wide tables)");
+  if ((e = hipMemcpy(c->d_wdir, dir.data(), dir.size() * sizeof(WideDir),
+                     hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy(wide dir)");
+  if ((e = hipMemcpy(c->d_wtab, tab.data(), tab.size() * sizeof(WideSlot),
+                     hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy(wide tables)");
+  c->wdir_log2 = dlg;
+  c->wide_min = (uint32_t)wmin;
+  c->wide_nodes = nodes.size();
+  c->wide_slots = slots;
   return FT_OK;
 }
 
@@ -188,6 +277,10 @@ int ft_create(const void* image, size_t image_bytes, int device,
   }
   c->ring.assign(2 * ft_ctx::kRing, nullptr);
   for (auto& ev : c->ring) (void)hipEventCreate(&ev);
+  if (int rc = build_wide_index(c, (const uint8_t*)image)) {
+    ft_destroy(c);
+    return rc;
+  }
   if (const char* s = std::getenv("FT_SCAN_MULT")) {
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
@@ -233,7 +326,8 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   L.cur_cap = (uint32_t)B;
   c->lay = L;
   c->ws_stride = off;
-  c->out_slot_max = align_up(sizeof(OutHeader) + 12 * B + 4 * (uint64_t)max_out_tokens, 256);
+  c->out_slot_max = align_up(step_stats_offset((uint32_t)B, 0) + 4 * (uint64_t)max_out_tokens +
+                                 8ull * kStepStats * max_steps + 8, 256);
   // per request: lnf + beams + ids + logps + row flags + permutation
   c->per_req = align_up(8 * (max_steps + 1), 16) + align_up(4 * max_steps, 16) +
                3 * align_up(4 * max_steps * K, 16) + align_up(max_steps, 16) + 256;
@@ -380,7 +474,7 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     st.T = T;
     st.K = K;
     st.F = F;
-    st.out_bytes = sizeof(OutHeader) + 12ull * F + 4ull * F * T;
+    st.out_bytes = step_stats_offset(F, T) + 8ull * kStepStats * T;
     max_out = std::max(max_out, st.out_bytes);
     D[r] = d;
   }
@@ -419,6 +513,10 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
   const uint64_t sl = (uint64_t)c->scan_mult * kmax;
   a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
+  a.wdir = c->d_wdir;
+  a.wtab = c->d_wtab;
+  a.wdir_log2 = c->wdir_log2;
+  a.wide_min = c->wide_min;
   (void)hipSetDevice(c->device);
   const size_t slot = (c->launches % ft_ctx::kRing) * 2;
   (void)hipEventRecord(c->ring[slot], c->stream);
@@ -545,6 +643,10 @@ int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
     }
     o.count = n;
     o.status = FT_OK;
+    if (o.step_stats) {
+      const uint64_t* ss = (const uint64_t*)(ob + step_stats_offset(st.F, st.T));
+      std::memcpy(o.step_stats, ss, 8ull * kStepStats * st.T);
+    }
   }
   if (timing) *timing = tm;
   return first_err;
@@ -565,6 +667,8 @@ void ft_destroy(ft_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   release_workspace(c);
   if (c->d_image) (void)hipFree(c->d_image);
+  if (c->d_wdir) (void)hipFree(c->d_wdir);
+  if (c->d_wtab) (void)hipFree(c->d_wtab);
   for (auto& ev : c->ring)
     if (ev) (void)hipEventDestroy(ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);

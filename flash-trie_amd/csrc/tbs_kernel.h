@@ -73,6 +73,33 @@ struct OutHeader {  // 64 bytes, then norms[F] f64, lengths[F], tokens[F*T]
 };
 static_assert(sizeof(OutHeader) == 64, "OutHeader layout");
 
+// Per-step profile written after the output tokens of each request:
+// parents, work items, next pushes, selected pushes, expansion ticks,
+// selection ticks, child records scanned, binary-search probes.
+constexpr uint32_t kStepStats = 8;
+__host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
+  return (sizeof(OutHeader) + 12ull * F + 4ull * F * T + 7) & ~7ull;
+}
+
+// Wide-node index, built by ft_create from the image: every node with at
+// least `wide_min` children gets an open-addressing table token -> child id
+// (load <= 1/2), found through a directory keyed by node id.  Both use
+// Fibonacci hashing and linear probing; 0xFFFFFFFF marks an empty slot.
+struct WideDir {
+  uint32_t node;
+  uint32_t log2size;
+  uint32_t slot_off;
+  uint32_t pad;
+};
+struct WideSlot {
+  uint32_t tok;
+  uint32_t child;
+};
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+__host__ __device__ inline uint32_t fib_slot(uint32_t x, uint32_t log2n) {
+  return log2n ? (uint32_t)((x * 0x9E3779B1u) >> (32 - log2n)) : 0u;
+}
+
 struct WsLayout {   // byte offsets inside one request's workspace slot
   uint64_t cur0, cur1, nextc, selA, selB, rank, hist;
   uint32_t next_cap, sel_cap, hist_cap, cur_cap;
@@ -91,6 +118,10 @@ struct KArgs {
   WsLayout lay;
   uint32_t batch;
   uint32_t scan_limit;
+  const WideDir* wdir;   // null: no wide-node index
+  const WideSlot* wtab;
+  uint32_t wdir_log2;
+  uint32_t wide_min;
 };
 
 // Launches the search over `batch` requests (one workgroup each) as a

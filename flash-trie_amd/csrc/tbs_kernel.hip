@@ -70,7 +70,8 @@ enum : uint8_t {
   M_LP_NEXT = 1,
   M_LP_SEL = 2,
   M_SCAN = 3,
-  M_SEARCH = 4
+  M_SEARCH = 4,
+  M_HASH = 5
 };
 
 __device__ __forceinline__ uint64_t norm_key(double v) {
@@ -335,6 +336,11 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
                  hist_cap = a.lay.hist_cap;
 
   unsigned long long t_exp = 0, t_sel = 0, t_all0 = wall_clock64();
+  // per-step profile rows after the output tokens: kStepStats u64 per step
+  uint64_t* step_stats =
+      (uint64_t*)(ob + step_stats_offset(d.F, d.out_T));
+  unsigned long long chunk_w = 0;
+  for (uint32_t i = tid; i < d.out_T * kStepStats; i += kBlock) step_stats[i] = 0;
   if (tid == 0) {
     cur[0].s = 0.0;
     cur[0].node = 0;
@@ -349,6 +355,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   for (uint32_t t = 0; t < T; ++t) {
     if (n_cur == 0 || (early && nS >= F)) break;
     const unsigned long long t0 = wall_clock64();
+    const unsigned long long ch0 = sm.cnt_children, pr0 = sm.cnt_probes;
+    const uint32_t ncur0 = n_cur;
+    chunk_w = 0;
     // ---- row t into LDS, ascending token order -------------------------
     const uint32_t* rid = ids + (uint64_t)t * K;
     const float* rlp = lps + (uint64_t)t * K;
@@ -378,7 +387,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         const uint32_t cend = a.recs[p.node + 1].child_begin;
         const uint32_t deg = cend - r.child_begin;
         const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
-        uint32_t aux = deg;
+        uint32_t aux = deg, pc0 = r.child_begin;
         if ((r.meta & FT_META_TERMINAL) && sd > t) {
           uint32_t err = 0;
           aux = kb_token(a, p.node, r, t, &err);
@@ -393,8 +402,24 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         } else {
           mode = M_SEARCH;
           work = K;
+          if (a.wdir && deg >= a.wide_min) {
+            // this node has a table: find it in the directory
+            const uint32_t mask = (1u << a.wdir_log2) - 1u;
+            uint32_t sl = fib_slot(p.node, a.wdir_log2);
+            for (uint32_t it = 0; it <= mask; ++it) {
+              const WideDir e = a.wdir[sl];
+              if (e.node == p.node) {
+                mode = M_HASH;
+                aux = e.log2size;
+                pc0 = e.slot_off;  // pc0 carries the table offset
+                break;
+              }
+              if (e.node == kEmpty) break;
+              sl = (sl + 1) & mask;
+            }
+          }
         }
-        sm.pc0[tid] = r.child_begin;
+        sm.pc0[tid] = pc0;
         sm.paux[tid] = aux;
         sm.pnode[tid] = p.node;
       }
@@ -403,6 +428,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       const uint32_t off = block_excl_scan(work, &W, sm);
       sm.woff[tid] = off;
       if (tid == 0) sm.woff[kBlock] = W;
+      chunk_w += W;
       if (tid == 0) sm.cnt_parents += min(n_cur - cbase, (uint32_t)kBlock);
       __syncthreads();
       const uint32_t nchunk = min(n_cur - cbase, (uint32_t)kBlock);
@@ -436,7 +462,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             ++my_children;
             pos = row_find(sm, K, cr.first_tok);
             have_child = true;
-          } else if (md == M_SEARCH) {
+          } else if (md == M_SEARCH || md == M_HASH) {
             pos = (int)q;
           }
           if (pos >= 0) {
@@ -463,6 +489,25 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
                     cnode = lo2;
                     have_child = true;
                   }
+                }
+              }
+              if (md == M_HASH) {
+                // open addressing in the parent's table
+                const uint32_t lg = sm.paux[jj];
+                const uint32_t mask = (1u << lg) - 1u;
+                const WideSlot* tab = a.wtab + sm.pc0[jj];
+                uint32_t sl = fib_slot(tok, lg);
+                for (uint32_t it = 0; it <= mask; ++it) {
+                  const WideSlot e = tab[sl];
+                  ++my_probes;
+                  if (e.tok == tok) {
+                    cnode = e.child;
+                    cr = a.recs[cnode];
+                    have_child = true;
+                    break;
+                  }
+                  if (e.tok == kEmpty) break;
+                  sl = (sl + 1) & mask;
                 }
               }
               if (md == M_LP_NEXT) {
@@ -522,6 +567,17 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
     const unsigned long long t1 = wall_clock64();
     t_exp += t1 - t0;
+    if (tid == 0 && t < d.out_T) {
+      uint64_t* row = step_stats + (uint64_t)t * kStepStats;
+      row[0] = ncur0;
+      row[1] = chunk_w;
+      row[2] = n_next;
+      row[3] = n_new;
+      row[4] = t1 - t0;
+      row[5] = 0;
+      row[6] = sm.cnt_children - ch0;
+      row[7] = sm.cnt_probes - pr0;
+    }
 
     // ---- parent ranks (only when arrival order is needed) ---------------
     bool ranks_done = false;
@@ -675,6 +731,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
     __syncthreads();
     n_cur = sm.n_out;
+    if (tid == 0 && t < d.out_T) step_stats[(uint64_t)t * kStepStats + 5] = wall_clock64() - t1;
     if (n_cur != keep_cnt) {  // the bound must keep exactly keep_cnt
       if (tid == 0) sm.status |= kStatusCorrupt;
       __syncthreads();

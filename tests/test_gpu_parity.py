@@ -240,3 +240,28 @@ def test_beam_1000(ft, po):
                             [lp[r].tolist()], -10.0, -40.0, 5.0, False)
         want = o.tbs([1000] * 10, ids[r], lp[r], -10.0, -40.0, 5.0, False)
         assert_same_results((got[0][0], got[1][0]), want, f"B1000 {r}")
+
+
+@pytest.mark.parametrize("scan_mult,wide_min", [("0", "0"), ("0", "2"),
+                                                ("1000000", "512"), ("1", "64")])
+def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min):
+    # scan_mult 0 sends every parent with children to the binary search
+    # (wide_min 0) or the hash tables (wide_min 2); 1000000 scans all
+    monkeypatch.setenv("FT_SCAN_MULT", scan_mult)
+    monkeypatch.setenv("FT_WIDE_MIN", wide_min)
+    toks, offs = ft.synth_keys(50000, 4096, 3, 8, 1.1, 4)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=32, steps=8,
+                  beams=16, inter=2048)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 24, 4096, 8, 32, 16, 0.3, 2.0, True, 4,
+                                model=1)
+    for b0 in range(0, 24, 4):
+        got = ft.bs_tbs_gpu(t, 4, [[16] * 8] * 4,
+                            [ids[b0 + i].tolist() for i in range(4)],
+                            [lp[b0 + i].tolist() for i in range(4)],
+                            -10.0, -40.0, 5.0, b0 % 8 == 4)
+        for i in range(4):
+            want = o.tbs([16] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0,
+                         b0 % 8 == 4)
+            assert_same_results((got[0][i], got[1][i]), want,
+                                f"modes {scan_mult}/{wide_min} req {b0 + i}")
