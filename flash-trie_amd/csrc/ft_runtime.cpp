@@ -81,6 +81,10 @@ struct ft_ctx {
   uint64_t out_stride = 0;
   bool launched = false;
   uint32_t scan_mult = 8;
+  uint32_t wgs_req = 64;      // workgroups per request (clamped to residency)
+  uint32_t share_min = 8192;  // work items from which a step is shared
+  int max_resident = 0;
+  uint32_t epoch = 0;
   // ring of (start, end) event pairs, one pair per launch
   static constexpr size_t kRing = 1024;
   std::vector<hipEvent_t> ring;
@@ -281,6 +285,19 @@ int ft_create(const void* image, size_t image_bytes, int device,
     ft_destroy(c);
     return rc;
   }
+  c->max_resident = tbs_max_resident_blocks(c->num_cus);
+  if (c->max_resident <= 0) {
+    ft_destroy(c);
+    return fail(FT_E_DEVICE, "ft_create: the search kernel cannot be resident");
+  }
+  if (const char* s = std::getenv("FT_WGS")) {
+    const long v = std::strtol(s, nullptr, 10);
+    if (v >= 1 && v <= 4096) c->wgs_req = (uint32_t)v;
+  }
+  if (const char* s = std::getenv("FT_SHARE_MIN")) {
+    const long v = std::strtol(s, nullptr, 10);
+    if (v >= 0) c->share_min = (uint32_t)v;
+  }
   if (const char* s = std::getenv("FT_SCAN_MULT")) {
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
@@ -320,6 +337,15 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   L.selB = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
   L.rank = off; off = align_up(off + B * 4, 256);
   L.hist = off; off = align_up(off + (uint64_t)max_inter_beams * sizeof(HistRec), 256);
+  L.ctl = off; off = align_up(off + sizeof(Ctl), 256);
+  L.par_c0 = off; off = align_up(off + B * 4, 256);
+  L.par_aux = off; off = align_up(off + B * 4, 256);
+  L.par_node = off; off = align_up(off + B * 4, 256);
+  L.par_mode = off; off = align_up(off + B * 4, 256);
+  L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
+  L.row_id = off; off = align_up(off + K * 4, 256);
+  L.row_lp = off; off = align_up(off + K * 4, 256);
+  L.row_k = off; off = align_up(off + K * 2, 256);
   L.next_cap = (uint32_t)BK;
   L.sel_cap = (uint32_t)(BK + B);
   L.hist_cap = (uint32_t)max_inter_beams;
@@ -513,6 +539,11 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
   const uint64_t sl = (uint64_t)c->scan_mult * kmax;
   a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
+  // helpers per request: as many as stay co-resident with the batch
+  const uint32_t fit = (uint32_t)std::max<int>(1, c->max_resident / (int)count);
+  a.wgs = std::max(1u, std::min(c->wgs_req, fit));
+  a.share_min = c->share_min;
+  a.epoch = ++c->epoch;
   a.wdir = c->d_wdir;
   a.wtab = c->d_wtab;
   a.wdir_log2 = c->wdir_log2;

@@ -100,8 +100,28 @@ __host__ __device__ inline uint32_t fib_slot(uint32_t x, uint32_t log2n) {
   return log2n ? (uint32_t)((x * 0x9E3779B1u) >> (32 - log2n)) : 0u;
 }
 
+// Per-request control block shared by the request's leader and helper
+// workgroups.  `go` and `done` sit on their own 128-byte lines.
+constexpr uint32_t kGoExit = 0xFFFFFFFFu;
+struct Ctl {
+  unsigned long long go;  // (launch epoch << 32) | generation of the shared step
+  uint32_t pad0[30];
+  uint32_t done;          // helpers finished with the current shared step
+  uint32_t pad1[31];
+  // the shared step, written by the leader before `go`
+  uint32_t t, W, n_par, nS;
+  uint32_t sel_which, cur_which, status, pad2;
+  // counters of the step (atomics)
+  uint32_t n_next, n_sel;
+  unsigned long long children, probes;
+  uint32_t pad3[18];
+};
+static_assert(sizeof(Ctl) == 384, "Ctl layout");
+
 struct WsLayout {   // byte offsets inside one request's workspace slot
   uint64_t cur0, cur1, nextc, selA, selB, rank, hist;
+  uint64_t ctl, par_c0, par_aux, par_node, par_mode, par_woff;
+  uint64_t row_id, row_lp, row_k;
   uint32_t next_cap, sel_cap, hist_cap, cur_cap;
 };
 
@@ -122,11 +142,18 @@ struct KArgs {
   const WideSlot* wtab;
   uint32_t wdir_log2;
   uint32_t wide_min;
+  uint32_t wgs;        // workgroups per request (1 leader + wgs-1 helpers)
+  uint32_t share_min;  // work items from which a step is shared
+  uint32_t epoch;      // launch counter (tags the control words)
+  uint32_t pad;
 };
 
-// Launches the search over `batch` requests (one workgroup each) as a
+// Launches the search over `batch` requests (wgs workgroups each) as a
 // cooperative launch on `stream`.
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
+
+// Workgroups of the search kernel that fit on the device at once.
+int tbs_max_resident_blocks(int num_cus);
 
 // Threads per workgroup of the search kernel.
 int tbs_block_threads();

@@ -48,12 +48,8 @@ struct Smem {
   uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
   uint16_t row_k[kMaxLdsTopk];
-  // expansion: one chunk of up to kBlock parents
+  // expansion: the work-item prefix of up to kBlock parents (LDS copy)
   uint32_t woff[kBlock + 1];
-  uint32_t pc0[kBlock];
-  uint32_t paux[kBlock];
-  uint32_t pnode[kBlock];
-  uint8_t pmode[kBlock];
   // selection
   uint32_t hist[256];
   uint32_t wsum[kWaves];
@@ -61,6 +57,8 @@ struct Smem {
   uint32_t n_next, n_sel, n_out, overflow;
   uint32_t status;
   unsigned long long cnt_parents, cnt_children, cnt_probes;
+  unsigned long long bcast;
+  uint32_t w_children, w_probes;
 };
 // rank scratch aliases the row arrays (used after expansion only)
 constexpr int kRankChunk = 1024;
@@ -301,20 +299,288 @@ __device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
   return (lo < K && sm.row_id[lo] == tok) ? (int)lo : -1;
 }
 
+// Relaxed / acquire / release accesses of the control words (agent scope:
+// the request's workgroups may sit on different XCDs).
+__device__ __forceinline__ unsigned long long ld_relaxed(const unsigned long long* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_release(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Upper bound on spin iterations of a wait (each sleeps ~64 cycles): far
+// beyond any step, so a wait only ends this way if the peer is gone.
+constexpr uint32_t kSpinLimit = 1u << 28;
+
+// Everything a workgroup needs to expand a range of work items of one step.
+struct StepView {
+  const CurRec* cur;
+  SelRec* sel;
+  NextRec* nextc;
+  const uint32_t* pc0;   // first child id, or the hash-table offset
+  const uint32_t* paux;  // degree, the link-parent token, or log2 table size
+  const uint32_t* pnode;
+  const uint32_t* pmode;
+  const uint32_t* woff;  // exclusive prefix of work items, n_par + 1 entries
+  Ctl* ctl;
+  uint32_t n_par, K, t, nS;
+  uint32_t next_cap, sel_cap;
+  double lnf_next;
+  float tok_thr;
+  double sent_thr;
+};
+
+// Expands work items [w0, w1): each is (parent, child) for a scanned parent,
+// (parent, proposal) for a searched or hashed parent, or the single pending
+// token of a link parent.  Pushes go to the request's global buffers.
+__device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
+                             uint32_t w1, Smem& sm) {
+  const uint32_t tid = threadIdx.x;
+  const bool lds_woff = v.n_par <= (uint32_t)kBlock;
+  if (lds_woff)
+    for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = v.woff[i];
+  if (tid == 0) {
+    sm.w_children = 0;
+    sm.w_probes = 0;
+  }
+  __syncthreads();
+  uint32_t my_children = 0, my_probes = 0;
+  const uint32_t K = v.K, t = v.t;
+  for (uint32_t wbase = w0; wbase < w1; wbase += kBlock) {
+    const uint32_t w = wbase + tid;
+    bool do_next = false, do_sel = false;
+    uint32_t cnode = 0, pj = 0, k = 0, tok = 0;
+    double s2 = 0.0;
+    if (w < w1) {
+      // parent of work item w: the last j with woff[j] <= w
+      uint32_t lo = 0, hi = v.n_par;
+      while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        const uint32_t o = lds_woff ? sm.woff[mid] : v.woff[mid];
+        if (o <= w) lo = mid; else hi = mid;
+      }
+      pj = lo;
+      const uint32_t q = w - (lds_woff ? sm.woff[pj] : v.woff[pj]);
+      const uint32_t md = v.pmode[pj];
+      const uint32_t c0 = v.pc0[pj], aux = v.paux[pj];
+      int pos = -1;
+      ft_node_rec cr;
+      bool have_child = false;
+      if (md == M_LP_NEXT || md == M_LP_SEL) {
+        pos = row_find(sm, K, aux);
+        cnode = v.pnode[pj];
+      } else if (md == M_SCAN) {
+        cnode = c0 + q;
+        cr = a.recs[cnode];
+        ++my_children;
+        pos = row_find(sm, K, cr.first_tok);
+        have_child = true;
+      } else if (md == M_SEARCH || md == M_HASH) {
+        pos = (int)q;
+      }
+      if (pos >= 0) {
+        const float x = sm.row_lp[pos];
+        k = sm.row_k[pos];
+        tok = sm.row_id[pos];
+        const double ps = v.cur[pj].s;
+        // thresholds in double, `<=` drops (louds-trie.cc:87-90)
+        const bool low = ((double)x <= (double)v.tok_thr) ||
+                         (ps + (double)x <= v.sent_thr);
+        if (!low) {
+          s2 = ps + (double)x;
+          if (md == M_SEARCH) {
+            // lower_bound of tok among the parent's children
+            uint32_t lo2 = c0, hi2 = c0 + aux;
+            const uint32_t end2 = hi2;
+            while (lo2 < hi2) {
+              const uint32_t mid = lo2 + ((hi2 - lo2) >> 1);
+              ++my_probes;
+              if (a.recs[mid].first_tok < tok) lo2 = mid + 1; else hi2 = mid;
+            }
+            if (lo2 < end2) {
+              cr = a.recs[lo2];
+              if (cr.first_tok == tok) {
+                cnode = lo2;
+                have_child = true;
+              }
+            }
+          } else if (md == M_HASH) {
+            // open addressing in the parent's table
+            const uint32_t mask = (1u << aux) - 1u;
+            const WideSlot* tab = a.wtab + c0;
+            uint32_t sl = fib_slot(tok, aux);
+            for (uint32_t it = 0; it <= mask; ++it) {
+              const WideSlot e = tab[sl];
+              ++my_probes;
+              if (e.tok == tok) {
+                cnode = e.child;
+                cr = a.recs[cnode];
+                have_child = true;
+                break;
+              }
+              if (e.tok == kEmpty) break;
+              sl = (sl + 1) & mask;
+            }
+          }
+          if (md == M_LP_NEXT) {
+            do_next = true;
+          } else if (md == M_LP_SEL) {
+            do_sel = true;
+          } else if (have_child) {
+            // terminal with |KB| == |Q| -> selected; always next
+            // (louds-trie.cc:103-108)
+            do_next = true;
+            do_sel = (cr.meta & FT_META_TERMINAL) &&
+                     ((cr.meta & FT_META_DEPTH_MASK) == t + 1);
+          }
+        }
+      }
+    }
+    // appends (every lane of the wave reaches these)
+    const uint32_t jk = (pj << 16) | k;
+    const uint32_t in_ = wave_append(do_next, &v.ctl->n_next);
+    if (do_next && in_ < v.next_cap) {
+      NextRec nr;
+      nr.key = norm_key(s2 * v.lnf_next);
+      nr.node = cnode;
+      nr.jk = jk;
+      v.nextc[in_] = nr;
+    }
+    const uint32_t is_ = wave_append(do_sel, &v.ctl->n_sel);
+    if (do_sel && v.nS + is_ < v.sel_cap) {
+      SelRec sr;
+      sr.s = s2;
+      sr.node = cnode;
+      sr.depth = t + 1;
+      sr.phist = v.cur[pj].hist;
+      sr.tok = tok;
+      sr.jk = jk;
+      sr.isnew = 1;
+      v.sel[v.nS + is_] = sr;
+    }
+  }
+  if (my_children) atomicAdd(&sm.w_children, my_children);
+  if (my_probes) atomicAdd(&sm.w_probes, my_probes);
+  __syncthreads();
+  if (tid == 0) {
+    if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
+    if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
+  }
+}
+
+// Loads the proposal row of step t into LDS in ascending token order.
+__device__ void load_row(const uint32_t* ids, const float* lps,
+                         const uint32_t* perm, bool permuted, uint32_t t,
+                         uint32_t K, Smem& sm) {
+  const uint32_t* rid = ids + (uint64_t)t * K;
+  const float* rlp = lps + (uint64_t)t * K;
+  for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
+    const uint32_t k = permuted ? perm[(uint64_t)t * K + p] : p;
+    sm.row_id[p] = rid[k];
+    sm.row_lp[p] = rlp[k];
+    sm.row_k[p] = (uint16_t)k;
+  }
+}
+
+// A helper workgroup: waits for shared steps of its request and expands its
+// slice of the work items, until the leader posts the exit generation.
+__device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
+                            uint32_t g, Smem& sm) {
+  const uint32_t tid = threadIdx.x;
+  Ctl* ctl = (Ctl*)(ws + a.lay.ctl);
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  unsigned long long seen = tag;  // generation 0: nothing posted yet
+  const uint8_t* in = a.stage + d.in_off;
+  const double* lnf = (const double*)in;
+  const uint32_t* ids = (const uint32_t*)(in + d.ids_off);
+  const float* lps = (const float*)(in + d.lp_off);
+  for (;;) {
+    if (tid == 0) {
+      unsigned long long v = 0;
+      for (uint32_t it = 0; it < kSpinLimit; ++it) {
+        v = ld_relaxed(&ctl->go);
+        if ((v >> 32) == a.epoch && v != seen) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      sm.bcast = v;
+    }
+    __syncthreads();
+    const unsigned long long v = sm.bcast;
+    __syncthreads();
+    if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
+    seen = v;
+    __threadfence();  // acquire the leader's step data
+    const uint32_t t = ld_relaxed(&ctl->t), W = ld_relaxed(&ctl->W);
+    StepView sv;
+    sv.cur = (const CurRec*)(ws + (ld_relaxed(&ctl->cur_which) ? a.lay.cur1 : a.lay.cur0));
+    sv.sel = (SelRec*)(ws + (ld_relaxed(&ctl->sel_which) ? a.lay.selB : a.lay.selA));
+    sv.nextc = (NextRec*)(ws + a.lay.nextc);
+    sv.pc0 = (const uint32_t*)(ws + a.lay.par_c0);
+    sv.paux = (const uint32_t*)(ws + a.lay.par_aux);
+    sv.pnode = (const uint32_t*)(ws + a.lay.par_node);
+    sv.pmode = (const uint32_t*)(ws + a.lay.par_mode);
+    sv.woff = (const uint32_t*)(ws + a.lay.par_woff);
+    sv.ctl = ctl;
+    sv.n_par = ld_relaxed(&ctl->n_par);
+    sv.K = d.K;
+    sv.t = t;
+    sv.nS = ld_relaxed(&ctl->nS);
+    sv.next_cap = a.lay.next_cap;
+    sv.sel_cap = a.lay.sel_cap;
+    sv.lnf_next = lnf[t + 1];
+    sv.tok_thr = d.tok_thr;
+    sv.sent_thr = d.sent_thr;
+    // the sorted row, as the leader published it
+    const uint32_t* gid = (const uint32_t*)(ws + a.lay.row_id);
+    const float* glp = (const float*)(ws + a.lay.row_lp);
+    const uint16_t* gk = (const uint16_t*)(ws + a.lay.row_k);
+    for (uint32_t p = tid; p < d.K; p += kBlock) {
+      sm.row_id[p] = gid[p];
+      sm.row_lp[p] = glp[p];
+      sm.row_k[p] = gk[p];
+    }
+    (void)ids;
+    (void)lps;
+    __syncthreads();
+    const uint64_t G = a.wgs;
+    const uint32_t w0 = (uint32_t)((uint64_t)W * g / G);
+    const uint32_t w1 = (uint32_t)((uint64_t)W * (g + 1) / G);
+    expand_range(a, sv, w0, w1, sm);
+    __threadfence();  // release this slice's pushes
+    __syncthreads();
+    if (tid == 0) atomicAdd(&ctl->done, 1u);
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   __shared__ Smem sm;
-  const uint32_t req = blockIdx.x;
+  // request-major interleave: request r owns blocks r, r + batch, ...
+  const uint32_t req = blockIdx.x % a.batch;
+  const uint32_t g = blockIdx.x / a.batch;
   const uint32_t tid = threadIdx.x;
-  if (req >= a.batch) return;
+  if (g >= a.wgs) return;
 
   const DevReq d = a.reqs[req];
   uint8_t* ws = a.ws + (uint64_t)req * a.ws_stride;
-  uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
-  OutHeader* oh = (OutHeader*)ob;
   if (d.flags & kReqSkip) {
-    if (tid == 0) { oh->count = 0; oh->status = 0; }
+    if (g == 0 && tid == 0) {
+      OutHeader* oh = (OutHeader*)(a.out + (uint64_t)req * a.out_stride);
+      oh->count = 0;
+      oh->status = 0;
+    }
     return;
   }
+  if (g != 0) {
+    helper_loop(a, d, ws, g, sm);
+    return;
+  }
+
+  // ---- the leader ----------------------------------------------------------
+  uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
+  OutHeader* oh = (OutHeader*)ob;
   const uint8_t* in = a.stage + d.in_off;
   const double* lnf = (const double*)in;
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
@@ -327,19 +593,26 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
 
   CurRec* cur = (CurRec*)(ws + a.lay.cur0);
   CurRec* cur2 = (CurRec*)(ws + a.lay.cur1);
+  uint32_t cur_which = 0, sel_which = 0;
   NextRec* nextc = (NextRec*)(ws + a.lay.nextc);
   SelRec* selA = (SelRec*)(ws + a.lay.selA);
   SelRec* selB = (SelRec*)(ws + a.lay.selB);
   uint32_t* rank = (uint32_t*)(ws + a.lay.rank);
   HistRec* hist = (HistRec*)(ws + a.lay.hist);
+  Ctl* ctl = (Ctl*)(ws + a.lay.ctl);
+  uint32_t* par_c0 = (uint32_t*)(ws + a.lay.par_c0);
+  uint32_t* par_aux = (uint32_t*)(ws + a.lay.par_aux);
+  uint32_t* par_node = (uint32_t*)(ws + a.lay.par_node);
+  uint32_t* par_mode = (uint32_t*)(ws + a.lay.par_mode);
+  uint32_t* par_woff = (uint32_t*)(ws + a.lay.par_woff);
   const uint32_t next_cap = a.lay.next_cap, sel_cap = a.lay.sel_cap,
                  hist_cap = a.lay.hist_cap;
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  uint32_t gen = 0;
 
   unsigned long long t_exp = 0, t_sel = 0, t_all0 = wall_clock64();
   // per-step profile rows after the output tokens: kStepStats u64 per step
-  uint64_t* step_stats =
-      (uint64_t*)(ob + step_stats_offset(d.F, d.out_T));
-  unsigned long long chunk_w = 0;
+  uint64_t* step_stats = (uint64_t*)(ob + step_stats_offset(d.F, d.out_T));
   for (uint32_t i = tid; i < d.out_T * kStepStats; i += kBlock) step_stats[i] = 0;
   if (tid == 0) {
     cur[0].s = 0.0;
@@ -355,40 +628,31 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   for (uint32_t t = 0; t < T; ++t) {
     if (n_cur == 0 || (early && nS >= F)) break;
     const unsigned long long t0 = wall_clock64();
-    const unsigned long long ch0 = sm.cnt_children, pr0 = sm.cnt_probes;
     const uint32_t ncur0 = n_cur;
-    chunk_w = 0;
-    // ---- row t into LDS, ascending token order -------------------------
-    const uint32_t* rid = ids + (uint64_t)t * K;
-    const float* rlp = lps + (uint64_t)t * K;
-    const bool permuted = perm && rowflag[t] != 0;
-    for (uint32_t p = tid; p < K; p += kBlock) {
-      const uint32_t k = permuted ? perm[(uint64_t)t * K + p] : p;
-      sm.row_id[p] = rid[k];
-      sm.row_lp[p] = rlp[k];
-      sm.row_k[p] = (uint16_t)k;
-    }
+    load_row(ids, lps, perm, perm && rowflag[t] != 0, t, K, sm);
     if (tid == 0) {
-      sm.n_next = 0;
-      sm.n_sel = 0;
-      sm.overflow = 0;
+      ctl->n_next = 0;
+      ctl->n_sel = 0;
+      ctl->children = 0;
+      ctl->probes = 0;
+      ctl->status = 0;
     }
     const double lnf_next = lnf[t + 1];
-    __syncthreads();
 
-    // ---- expansion ------------------------------------------------------
+    // ---- parents: lookup mode, work items, exclusive prefix ---------------
+    uint32_t W = 0;
     for (uint32_t cbase = 0; cbase < n_cur; cbase += kBlock) {
       const uint32_t j = cbase + tid;
       uint32_t work = 0;
-      uint8_t mode = M_NONE;
       if (j < n_cur) {
         const CurRec p = cur[j];
         const ft_node_rec r = a.recs[p.node];
         const uint32_t cend = a.recs[p.node + 1].child_begin;
         const uint32_t deg = cend - r.child_begin;
         const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
-        uint32_t aux = deg, pc0 = r.child_begin;
+        uint32_t aux = deg, pc0 = r.child_begin, mode = M_NONE;
         if ((r.meta & FT_META_TERMINAL) && sd > t) {
+          // link parent: only KB(n)[|Q|] extends it (louds-trie.cc:91-102)
           uint32_t err = 0;
           aux = kb_token(a, p.node, r, t, &err);
           if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
@@ -411,7 +675,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
               if (e.node == p.node) {
                 mode = M_HASH;
                 aux = e.log2size;
-                pc0 = e.slot_off;  // pc0 carries the table offset
+                pc0 = e.slot_off;
                 break;
               }
               if (e.node == kEmpty) break;
@@ -419,164 +683,105 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             }
           }
         }
-        sm.pc0[tid] = pc0;
-        sm.paux[tid] = aux;
-        sm.pnode[tid] = p.node;
+        par_c0[j] = pc0;
+        par_aux[j] = aux;
+        par_node[j] = p.node;
+        par_mode[j] = mode;
       }
-      sm.pmode[tid] = mode;
-      uint32_t W;
-      const uint32_t off = block_excl_scan(work, &W, sm);
-      sm.woff[tid] = off;
-      if (tid == 0) sm.woff[kBlock] = W;
-      chunk_w += W;
-      if (tid == 0) sm.cnt_parents += min(n_cur - cbase, (uint32_t)kBlock);
-      __syncthreads();
-      const uint32_t nchunk = min(n_cur - cbase, (uint32_t)kBlock);
-      uint32_t my_children = 0, my_probes = 0;
-      for (uint32_t wbase = 0; wbase < W; wbase += kBlock) {
-        const uint32_t w = wbase + tid;
-        bool do_next = false, do_sel = false;
-        uint32_t cnode = 0, jj = 0, k = 0, tok = 0;
-        double s2 = 0.0;
-        uint32_t cdepth = t + 1;
-        if (w < W) {
-          // parent of work item w: last jj with woff[jj] <= w
-          uint32_t lo = 0, hi = nchunk;
-          while (hi - lo > 1) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (sm.woff[mid] <= w) lo = mid; else hi = mid;
-          }
-          jj = lo;
-          const uint32_t q = w - sm.woff[jj];
-          const uint8_t md = sm.pmode[jj];
-          const uint32_t pj = cbase + jj;
-          int pos = -1;
-          ft_node_rec cr;
-          bool have_child = false;
-          if (md == M_LP_NEXT || md == M_LP_SEL) {
-            pos = row_find(sm, K, sm.paux[jj]);
-            cnode = sm.pnode[jj];
-          } else if (md == M_SCAN) {
-            cnode = sm.pc0[jj] + q;
-            cr = a.recs[cnode];
-            ++my_children;
-            pos = row_find(sm, K, cr.first_tok);
-            have_child = true;
-          } else if (md == M_SEARCH || md == M_HASH) {
-            pos = (int)q;
-          }
-          if (pos >= 0) {
-            const float x = sm.row_lp[pos];
-            k = sm.row_k[pos];
-            tok = sm.row_id[pos];
-            const double ps = cur[pj].s;
-            const bool low = ((double)x <= (double)d.tok_thr) ||
-                             (ps + (double)x <= d.sent_thr);
-            if (!low) {
-              s2 = ps + (double)x;
-              if (md == M_SEARCH) {
-                // lower_bound of tok among the parent's children
-                uint32_t lo2 = sm.pc0[jj], hi2 = sm.pc0[jj] + sm.paux[jj];
-                const uint32_t end2 = hi2;
-                while (lo2 < hi2) {
-                  const uint32_t mid = lo2 + ((hi2 - lo2) >> 1);
-                  ++my_probes;
-                  if (a.recs[mid].first_tok < tok) lo2 = mid + 1; else hi2 = mid;
-                }
-                if (lo2 < end2) {
-                  cr = a.recs[lo2];
-                  if (cr.first_tok == tok) {
-                    cnode = lo2;
-                    have_child = true;
-                  }
-                }
-              }
-              if (md == M_HASH) {
-                // open addressing in the parent's table
-                const uint32_t lg = sm.paux[jj];
-                const uint32_t mask = (1u << lg) - 1u;
-                const WideSlot* tab = a.wtab + sm.pc0[jj];
-                uint32_t sl = fib_slot(tok, lg);
-                for (uint32_t it = 0; it <= mask; ++it) {
-                  const WideSlot e = tab[sl];
-                  ++my_probes;
-                  if (e.tok == tok) {
-                    cnode = e.child;
-                    cr = a.recs[cnode];
-                    have_child = true;
-                    break;
-                  }
-                  if (e.tok == kEmpty) break;
-                  sl = (sl + 1) & mask;
-                }
-              }
-              if (md == M_LP_NEXT) {
-                do_next = true;
-              } else if (md == M_LP_SEL) {
-                do_sel = true;
-              } else if (have_child) {
-                do_next = true;
-                do_sel = (cr.meta & FT_META_TERMINAL) &&
-                         ((cr.meta & FT_META_DEPTH_MASK) == t + 1);
-              }
-            }
-          }
-        }
-        // appends (all lanes of the wave reach these)
-        const uint32_t jk = ((cbase + jj) << 16) | k;
-        const uint32_t in_ = wave_append(do_next, &sm.n_next);
-        if (do_next) {
-          if (in_ < next_cap) {
-            NextRec nr;
-            nr.key = norm_key(s2 * lnf_next);
-            nr.node = cnode;
-            nr.jk = jk;
-            nextc[in_] = nr;
-          } else {
-            atomicOr(&sm.overflow, 1u);
-          }
-        }
-        const uint32_t is_ = wave_append(do_sel, &sm.n_sel);
-        if (do_sel) {
-          const uint32_t slot = nS + is_;
-          if (slot < sel_cap) {
-            SelRec sr;
-            sr.s = s2;
-            sr.node = cnode;
-            sr.depth = cdepth;
-            sr.phist = cur[cbase + jj].hist;
-            sr.tok = tok;
-            sr.jk = jk;
-            sr.isnew = 1;
-            selA[slot] = sr;
-          } else {
-            atomicOr(&sm.overflow, 1u);
-          }
-        }
-      }
-      if (my_children) atomicAdd(&sm.cnt_children, (unsigned long long)my_children);
-      if (my_probes) atomicAdd(&sm.cnt_probes, (unsigned long long)my_probes);
-      __syncthreads();
+      uint32_t Wc;
+      const uint32_t off = block_excl_scan(work, &Wc, sm);
+      if (j < n_cur) par_woff[j] = W + off;
+      W += Wc;
     }
-    const uint32_t n_next = sm.n_next, n_new = sm.n_sel;
+    if (tid == 0) {
+      par_woff[n_cur] = W;
+      sm.cnt_parents += n_cur;
+    }
+    __syncthreads();
+
+    StepView sv;
+    sv.cur = cur;
+    sv.sel = selA;
+    sv.nextc = nextc;
+    sv.pc0 = par_c0;
+    sv.paux = par_aux;
+    sv.pnode = par_node;
+    sv.pmode = par_mode;
+    sv.woff = par_woff;
+    sv.ctl = ctl;
+    sv.n_par = n_cur;
+    sv.K = K;
+    sv.t = t;
+    sv.nS = nS;
+    sv.next_cap = next_cap;
+    sv.sel_cap = sel_cap;
+    sv.lnf_next = lnf_next;
+    sv.tok_thr = d.tok_thr;
+    sv.sent_thr = d.sent_thr;
+
+    const bool shared = a.wgs > 1 && W >= a.share_min;
+    uint32_t w_end = W;
+    if (shared) {
+      // publish the row and the step, then wake the helpers
+      uint32_t* gid = (uint32_t*)(ws + a.lay.row_id);
+      float* glp = (float*)(ws + a.lay.row_lp);
+      uint16_t* gk = (uint16_t*)(ws + a.lay.row_k);
+      for (uint32_t p = tid; p < K; p += kBlock) {
+        gid[p] = sm.row_id[p];
+        glp[p] = sm.row_lp[p];
+        gk[p] = sm.row_k[p];
+      }
+      if (tid == 0) {
+        ctl->t = t;
+        ctl->W = W;
+        ctl->n_par = n_cur;
+        ctl->nS = nS;
+        ctl->sel_which = sel_which;
+        ctl->cur_which = cur_which;
+        ctl->done = 0;
+      }
+      __threadfence();
+      __syncthreads();
+      if (tid == 0) st_release(&ctl->go, tag | ++gen);
+      w_end = (uint32_t)((uint64_t)W / a.wgs);
+    }
+    expand_range(a, sv, 0, w_end, sm);
+    if (shared) {
+      if (tid == 0) {
+        for (uint32_t it = 0; it < kSpinLimit; ++it) {
+          if (ld_relaxed(&ctl->done) >= a.wgs - 1) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (ld_relaxed(&ctl->done) < a.wgs - 1) sm.status |= kStatusCorrupt;
+      }
+      __syncthreads();
+      __threadfence();  // acquire the helpers' pushes
+    }
+    const uint32_t n_next = ld_relaxed(&ctl->n_next);
+    const uint32_t n_new = ld_relaxed(&ctl->n_sel);
+    const unsigned long long w_ch = ld_relaxed(&ctl->children);
+    const unsigned long long w_pr = ld_relaxed(&ctl->probes);
+    __syncthreads();
     n_cands += (uint64_t)n_next + n_new;
-    if (sm.overflow || sm.status) {
-      if (tid == 0) sm.status |= sm.overflow ? kStatusOverflow : 0u;
-      __syncthreads();
-      break;
+    if (tid == 0) {
+      sm.cnt_children += w_ch;
+      sm.cnt_probes += w_pr;
+      if (n_next > next_cap || nS + n_new > sel_cap) sm.status |= kStatusOverflow;
     }
+    __syncthreads();
+    if (sm.status) break;
     const unsigned long long t1 = wall_clock64();
     t_exp += t1 - t0;
     if (tid == 0 && t < d.out_T) {
       uint64_t* row = step_stats + (uint64_t)t * kStepStats;
       row[0] = ncur0;
-      row[1] = chunk_w;
+      row[1] = W;
       row[2] = n_next;
       row[3] = n_new;
       row[4] = t1 - t0;
       row[5] = 0;
-      row[6] = sm.cnt_children - ch0;
-      row[7] = sm.cnt_probes - pr0;
+      row[6] = w_ch;
+      row[7] = w_pr;
     }
 
     // ---- parent ranks (only when arrival order is needed) ---------------
@@ -676,6 +881,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         __syncthreads();
         nS = sm.n_out;
         SelRec* tmp = selA; selA = selB; selB = tmp;
+        sel_which ^= 1u;
         if (nS > F) {  // the bound keeps at most F
           if (tid == 0) sm.status |= kStatusCorrupt;
           __syncthreads();
@@ -740,13 +946,15 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     hist_used += n_cur;
     {
       CurRec* tmp = cur; cur = cur2; cur2 = tmp;
+      cur_which ^= 1u;
     }
     t_sel += wall_clock64() - t1;
     __syncthreads();
   }
+  // release the helpers
+  if (tid == 0) st_release(&ctl->go, tag | kGoExit);
 
   // ---- output: selected in ascending (norm, node id) -----------------------
-  const unsigned long long t2 = wall_clock64();
   double* onorm = (double*)(ob + sizeof(OutHeader));
   uint32_t* olen = (uint32_t*)(onorm + F);
   uint32_t* otok = olen + F;
@@ -810,16 +1018,24 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     oh->parents = sm.cnt_parents;
     oh->children = sm.cnt_children;
     oh->probes = sm.cnt_probes;
-    (void)t2;
   }
 }
 
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
   void* params[] = {(void*)&args};
-  return hipLaunchCooperativeKernel((const void*)tbs_kernel, dim3(args.batch),
-                                    dim3(kBlock), params, 0, stream);
+  return hipLaunchCooperativeKernel((const void*)tbs_kernel,
+                                    dim3(args.batch * args.wgs), dim3(kBlock),
+                                    params, 0, stream);
 }
 
 int tbs_block_threads() { return kBlock; }
+
+int tbs_max_resident_blocks(int num_cus) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)tbs_kernel,
+                                                   kBlock, 0) != hipSuccess)
+    return 0;
+  return per_cu * num_cus;
+}
 
 }  // namespace ftk

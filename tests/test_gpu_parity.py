@@ -265,3 +265,29 @@ def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min):
                          b0 % 8 == 4)
             assert_same_results((got[0][i], got[1][i]), want,
                                 f"modes {scan_mult}/{wide_min} req {b0 + i}")
+
+
+@pytest.mark.parametrize("wgs,share_min", [("2", "0"), ("7", "0"), ("64", "0"),
+                                           ("32", "100")])
+def test_shared_steps(ft, po, monkeypatch, wgs, share_min):
+    # steps expanded by a leader plus helper workgroups (share_min 0: every
+    # step is shared), with ties and early exit
+    monkeypatch.setenv("FT_WGS", wgs)
+    monkeypatch.setenv("FT_SHARE_MIN", share_min)
+    toks, offs = ft.synth_keys(80000, 8192, 3, 8, 1.1, 6)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=64, steps=8,
+                  beams=32, inter=4096)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 16, 8192, 8, 64, 32, 0.3, 2.0, True, 8,
+                                model=1)
+    for b0 in range(0, 16, 4):
+        for alpha, early in ((5.0, False), (1e6, False), (5.0, True)):
+            got = ft.bs_tbs_gpu(t, 4, [[32] * 8] * 4,
+                                [ids[b0 + i].tolist() for i in range(4)],
+                                [lp[b0 + i].tolist() for i in range(4)],
+                                -10.0, -40.0, alpha, early)
+            for i in range(4):
+                want = o.tbs([32] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0,
+                             alpha, early)
+                assert_same_results((got[0][i], got[1][i]), want,
+                                    f"wgs {wgs} req {b0 + i} {alpha} {early}")
