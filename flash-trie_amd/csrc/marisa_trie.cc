@@ -365,7 +365,11 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
     res[b].length = lens[b].data();
     res[b].tokens = toks[b].data();
   }
-  const int rc = ft_search(t.ctx, reqs.data(), B, res.data(), nullptr);
+  int rc;
+  {
+    std::lock_guard<std::mutex> lock(t.search_mu);
+    rc = ft_search(t.ctx, reqs.data(), B, res.data(), nullptr);
+  }
   if (rc) throw_ft(rc, "tbs_gpu_batched");
   for (size_t b = 0; b < B; ++b) {
     TbsInput& in = inputs[b];

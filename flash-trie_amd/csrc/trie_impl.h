@@ -2,6 +2,7 @@
 #pragma once
 
 #include <cstddef>
+#include <mutex>
 
 #include "../../include/flashtrie_amd.h"
 #include "image_builder.h"
@@ -14,6 +15,9 @@ class TrieImpl {
   ft_ctx* ctx = nullptr;  // created by init_tbs_gpu
   size_t max_batch = 0;
   size_t max_topk = 0, max_outpos = 0, max_out_beams = 0;
+  // One context has one workspace and one stream: searches on one trie run
+  // one at a time (the Python module releases the GIL around them).
+  std::mutex search_mu;
   ~TrieImpl() { drop_gpu(); }
   void drop_gpu() {
     if (ctx) ft_destroy(ctx);
