@@ -26,6 +26,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config paper]
 import argparse
 import json
 import os
+import re
 import sys
 import threading
 import time
@@ -62,6 +63,22 @@ def parse():
     p.add_argument("--boundary", type=int, default=100,
                    help="batch-1 requests timed through the C++ boundary")
     return p.parse_args()
+
+
+def measured_traffic(cfg, batch):
+    """HBM bytes per launch of the search kernel at this batch size, as
+    measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs and scaled by the same
+    counters of a copy kernel of known size; read from the committed counter
+    summary (None when it holds no figure for this workload and batch)."""
+    path = os.path.join(ROOT, "profiles", f"tbs_kernel_{cfg}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    pat = re.compile(r"^traffic_bytes_per_launch\[(\d+)\]\s*=\s*(\d+)")
+    for line in open(path):
+        m = pat.match(line.strip())
+        if m and int(m.group(1)) == batch:
+            return int(m.group(2))
+    return None
 
 
 def build_workload(ft, cfg, beam):
@@ -120,8 +137,13 @@ def main():
 
     # ---- device-resident throughput and latency per batch size ----------
     qps, kern_ms, results = {}, {}, {}
-    for b in batches:
+    for bi, b in enumerate(batches):
         nb = P // b
+        if bi:
+            # one untimed batch-3 launch between batch sizes: its grid size
+            # differs from every timed one, so a kernel trace splits into one
+            # run of dispatches per batch size
+            ft.launch(trie, 0, min(3, P))
         for i in range(args.warmup):
             ft.launch(trie, (i % nb) * b, b)
         ft.sync(trie)
@@ -175,7 +197,9 @@ def main():
         c1, n1, l1, t1, _ = ft.fetch(trie)
         bl.append((time.perf_counter() - t0) * 1e3)
     bl = np.array(bl)
-    log(f"boundary latency: mean {bl.mean():.3f} ms p99 {np.percentile(bl, 99):.3f} ms")
+    if bl.size:
+        log(f"boundary latency: mean {bl.mean():.3f} ms p99 "
+            f"{np.percentile(bl, 99):.3f} ms")
 
     # ---- CPU oracle baseline on a bounded sample + parity spot check -------
     cpu = None
@@ -272,7 +296,8 @@ def main():
         achieved = algo_bytes * peak_b / (kb.mean() * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 3),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "frac": achieved / HBM_PEAK_GBS,
+                "traffic": measured_traffic(args.config, peak_b),
                 "algorithmic_bytes_per_request": round(algo_bytes),
                 "requests_per_launch": peak_b}
     k1 = kern_ms.get(1, kb)
@@ -299,8 +324,10 @@ def main():
                    "thresholds": [TOK_THR, SENT_THR], "length_norm": ALPHA},
         "latency_ms": {"mean": round(float(k1.mean()), 4),
                        "p99": round(float(np.percentile(k1, 99)), 4),
-                       "boundary_mean": round(float(bl.mean()), 4),
-                       "boundary_p99": round(float(np.percentile(bl, 99)), 4)},
+                       "boundary_mean": (round(float(bl.mean()), 4)
+                                         if bl.size else None),
+                       "boundary_p99": (round(float(np.percentile(bl, 99)), 4)
+                                        if bl.size else None)},
         "qps_by_batch": {str(b): round(v, 1) for b, v in qps.items()},
         "kernel_ms_by_batch": {str(b): round(float(v.mean()), 4)
                                for b, v in kern_ms.items()},

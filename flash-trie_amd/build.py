@@ -4,6 +4,7 @@ Outputs, next to this file:
   libflashtrie_amd.so   C ABI + HIP kernels (hipcc, gfx950)
   libmarisa_amd.so      drop-in marisa::Trie, image builder, generators (g++)
   flashtrie*.so         the `flashtrie` Python module (pybind11)
+  ft_copy_calib         plain copy kernel of known size (HBM counter scale)
 
 Run ``python flash-trie_amd/build.py`` or call ``build()``.
 """
@@ -34,6 +35,7 @@ CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-ffp-contract=off",
 
 LIB_AMD = os.path.join(HERE, "libflashtrie_amd.so")
 LIB_MARISA = os.path.join(HERE, "libmarisa_amd.so")
+COPY_CALIB = os.path.join(HERE, "ft_copy_calib")
 
 
 def ext_suffix():
@@ -80,6 +82,8 @@ def build(verbose=False):
     for src, obj in host_objs.items():
         jobs.append([CXX] + CXX_FLAGS + ["-c", os.path.join(CSRC, src),
                                          "-o", obj])
+    jobs.append([HIPCC] + HIP_FLAGS + ["-x", "hip", os.path.join(CSRC, "copy_calib.hip"),
+                                       "-o", COPY_CALIB])
     jobs.append([CXX] + CXX_FLAGS + _pybind_includes() +
                 ["-fvisibility=hidden", "-c", os.path.join(CSRC, "bindings.cc"),
                  "-o", bind_obj])
@@ -97,7 +101,7 @@ def build(verbose=False):
     _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", PYMOD, bind_obj,
           "-L" + HERE, "-lmarisa_amd", "-lflashtrie_amd",
           "-Wl,-rpath,$ORIGIN"])
-    return [LIB_AMD, LIB_MARISA, PYMOD]
+    return [LIB_AMD, LIB_MARISA, PYMOD, COPY_CALIB]
 
 
 def built():
