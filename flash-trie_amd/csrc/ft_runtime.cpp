@@ -15,6 +15,8 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -73,9 +75,9 @@ struct ft_ctx {
 
   // wide-node index (device)
   WideDir* d_wdir = nullptr;
-  WideSlot* d_wtab = nullptr;
+  WideBucket* d_wtab = nullptr;
   uint32_t wdir_log2 = 0, wide_min = 0;
-  uint64_t wide_nodes = 0, wide_slots = 0;
+  uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
 
   std::vector<StagedReq> staged;
   uint64_t out_stride = 0;
@@ -123,6 +125,36 @@ static int alloc_staging(ft_ctx* c, size_t n) {
   return FT_OK;
 }
 
+// Cuckoo insertion of (token word, child) into a node's table: place it in
+// a free slot of one of its two buckets, else displace a random occupant of
+// one of them and re-insert that one.  False after `max_kicks` displacements
+// (the table is then unusable and the node falls back to binary search).
+static bool cuckoo_insert(WideBucket* tb, uint32_t lg, uint32_t tokw,
+                          uint32_t child, uint64_t* rng) {
+  constexpr int max_kicks = 4096;
+  for (int kick = 0; kick < max_kicks; ++kick) {
+    const uint32_t tok = tokw & kTokMask;
+    const uint32_t b1 = cuckoo_h1(tok, lg), b2 = cuckoo_h2(tok, lg);
+    for (const uint32_t b : {b1, b2})
+      for (int sl = 0; sl < 4; ++sl)
+        if (tb[b].child[sl] == 0) {
+          tb[b].tok[sl] = tokw;
+          tb[b].child[sl] = child;
+          return true;
+        }
+    uint64_t x = *rng;  // xorshift64
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *rng = x;
+    const uint32_t b = (x & 1) ? b1 : b2;
+    const int sl = (int)((x >> 1) & 3);
+    std::swap(tokw, tb[b].tok[sl]);
+    std::swap(child, tb[b].child[sl]);
+  }
+  return false;
+}
+
 // Builds the wide-node index on the host (parallel) and uploads it.
 static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   const char* env = std::getenv("FT_WIDE_MIN");
@@ -147,25 +179,20 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   for (auto& f : found) nodes.insert(nodes.end(), f.begin(), f.end());
   if (nodes.empty()) return FT_OK;
   std::vector<WideDir> ent(nodes.size());
-  uint64_t slots = 0;
+  uint64_t buckets = 0;
   for (size_t i = 0; i < nodes.size(); ++i) {
     const uint32_t n = nodes[i];
     const uint64_t deg = R[n + 1].child_begin - R[n].child_begin;
     uint32_t lg = 1;
-    while ((1ull << lg) < 2 * deg) ++lg;
-    ent[i] = WideDir{n, lg, (uint32_t)slots, 0};
-    slots += 1ull << lg;
+    while ((2ull << lg) < deg) ++lg;  // 4 slots a bucket, load <= 1/2
+    ent[i] = WideDir{n, lg, (uint32_t)buckets, 0};
+    buckets += 1ull << lg;
+    if (buckets >= 0xFFFFFFF0ull) return fail(FT_E_IMAGE, "wide-node index too large");
   }
-  if (slots >= 0xFFFFFFF0ull) return fail(FT_E_IMAGE, "wide-node index too large");
-  uint32_t dlg = 1;
-  while ((1ull << dlg) < 2 * nodes.size()) ++dlg;
-  std::vector<WideDir> dir(1ull << dlg, WideDir{kEmpty, 0, 0, 0});
-  for (const WideDir& e : ent) {
-    uint32_t sl = fib_slot(e.node, dlg);
-    while (dir[sl].node != kEmpty) sl = (sl + 1) & ((1u << dlg) - 1);
-    dir[sl] = e;
-  }
-  std::vector<WideSlot> tab(slots, WideSlot{kEmpty, 0});
+  // uninitialised: every table is cleared by the thread that fills it
+  std::unique_ptr<WideBucket[]> tab(new (std::nothrow) WideBucket[buckets]);
+  if (!tab) return fail(FT_E_NOMEM, "wide-node index: host memory");
+  std::vector<uint8_t> failed(ent.size(), 0);
   {
     std::atomic<size_t> next{0};
     std::vector<std::thread> th;
@@ -175,32 +202,50 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
           const size_t i = next.fetch_add(1);
           if (i >= ent.size()) break;
           const WideDir& e = ent[i];
-          WideSlot* t = tab.data() + e.slot_off;
-          const uint32_t mask = (1u << e.log2size) - 1;
+          WideBucket* tb = tab.get() + e.bucket_off;
+          std::memset(tb, 0, sizeof(WideBucket) << e.log2nb);
+          uint64_t rng = 0x9E3779B97F4A7C15ull ^ ((uint64_t)e.node << 1);
           for (uint32_t ch = R[e.node].child_begin; ch < R[e.node + 1].child_begin; ++ch) {
-            uint32_t sl = fib_slot(R[ch].first_tok, e.log2size);
-            while (t[sl].tok != kEmpty) sl = (sl + 1) & mask;
-            t[sl] = WideSlot{R[ch].first_tok, ch};
+            const uint32_t meta = R[ch].meta;
+            const uint32_t elen = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+            const bool sel = (meta & FT_META_TERMINAL) && elen == 1;
+            const uint32_t tokw = (R[ch].first_tok & kTokMask) | (sel ? kSlotSel : 0u);
+            if (!cuckoo_insert(tb, e.log2nb, tokw, ch, &rng)) {
+              failed[i] = 1;
+              break;
+            }
           }
         }
       });
     for (auto& x : th) x.join();
   }
+  uint64_t n_ok = 0;
+  for (size_t i = 0; i < ent.size(); ++i) n_ok += failed[i] ? 0 : 1;
+  uint32_t dlg = 1;
+  while ((1ull << dlg) < 2 * std::max<uint64_t>(n_ok, 1)) ++dlg;
+  std::vector<WideDir> dir(1ull << dlg, WideDir{kEmpty, 0, 0, 0});
+  for (size_t i = 0; i < ent.size(); ++i) {
+    if (failed[i]) continue;  // searched by binary search instead
+    uint32_t sl = fib_slot(ent[i].node, dlg);
+    while (dir[sl].node != kEmpty) sl = (sl + 1) & ((1u << dlg) - 1);
+    dir[sl] = ent[i];
+  }
   hipError_t e;
   if ((e = hipMalloc(&c->d_wdir, dir.size() * sizeof(WideDir))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide dir)");
-  if ((e = hipMalloc(&c->d_wtab, tab.size() * sizeof(WideSlot))) != hipSuccess)
+  if ((e = hipMalloc(&c->d_wtab, buckets * sizeof(WideBucket))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide tables)");
   if ((e = hipMemcpy(c->d_wdir, dir.data(), dir.size() * sizeof(WideDir),
                      hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(e, "hipMemcpy(wide dir)");
-  if ((e = hipMemcpy(c->d_wtab, tab.data(), tab.size() * sizeof(WideSlot),
+  if ((e = hipMemcpy(c->d_wtab, tab.get(), buckets * sizeof(WideBucket),
                      hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(e, "hipMemcpy(wide tables)");
   c->wdir_log2 = dlg;
   c->wide_min = (uint32_t)wmin;
-  c->wide_nodes = nodes.size();
-  c->wide_slots = slots;
+  c->wide_nodes = n_ok;
+  c->wide_buckets = buckets;
+  c->wide_failed = ent.size() - n_ok;
   return FT_OK;
 }
 

@@ -82,22 +82,41 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 }
 
 // Wide-node index, built by ft_create from the image: every node with at
-// least `wide_min` children gets an open-addressing table token -> child id
-// (load <= 1/2), found through a directory keyed by node id.  Both use
-// Fibonacci hashing and linear probing; 0xFFFFFFFF marks an empty slot.
+// least `wide_min` children gets a two-choice bucketed cuckoo table
+// token -> child id: 2^log2nb buckets of 4 slots (32 bytes, average load
+// <= 1/2).  A token sits in bucket h1(tok) or h2(tok), so a lookup reads two
+// buckets, independently, in one memory round trip whatever the table's
+// history of collisions.  A slot's token word carries kSlotSel when the
+// child can close a key one token below its parent (terminal, one-token
+// edge); an empty slot has child 0 (the root is nobody's child).  Tables are
+// found through a directory keyed by node id (Fibonacci hashing, linear
+// probing, node 0xFFFFFFFF marks an empty entry).
 struct WideDir {
   uint32_t node;
-  uint32_t log2size;
-  uint32_t slot_off;
+  uint32_t log2nb;      // log2 of the bucket count (>= 1)
+  uint32_t bucket_off;  // first bucket of the node's table
   uint32_t pad;
 };
-struct WideSlot {
-  uint32_t tok;
-  uint32_t child;
+struct WideBucket {
+  uint32_t tok[4];
+  uint32_t child[4];
 };
+static_assert(sizeof(WideBucket) == 32, "WideBucket layout");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+constexpr uint32_t kSlotSel = 0x80000000u;
+constexpr uint32_t kTokMask = 0x7FFFFFFFu;
 __host__ __device__ inline uint32_t fib_slot(uint32_t x, uint32_t log2n) {
   return log2n ? (uint32_t)((x * 0x9E3779B1u) >> (32 - log2n)) : 0u;
+}
+__host__ __device__ inline uint32_t cuckoo_h1(uint32_t tok, uint32_t lg) {
+  return (tok * 0x9E3779B1u) >> (32 - lg);
+}
+__host__ __device__ inline uint32_t cuckoo_h2(uint32_t tok, uint32_t lg) {
+  uint32_t h = (tok ^ 0x2545F491u) * 0x85EBCA6Bu;
+  h ^= h >> 13;
+  h *= 0xC2B2AE35u;
+  const uint32_t b = h >> (32 - lg);
+  return b == cuckoo_h1(tok, lg) ? b ^ 1u : b;
 }
 
 // Per-request control block shared by the request's leader and helper
@@ -139,7 +158,7 @@ struct KArgs {
   uint32_t batch;
   uint32_t scan_limit;
   const WideDir* wdir;   // null: no wide-node index
-  const WideSlot* wtab;
+  const WideBucket* wtab;
   uint32_t wdir_log2;
   uint32_t wide_min;
   uint32_t wgs;        // workgroups per request (1 leader + wgs-1 helpers)

@@ -48,8 +48,16 @@ struct Smem {
   uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
   uint16_t row_k[kMaxLdsTopk];
-  // expansion: the work-item prefix of up to kBlock parents (LDS copy)
+  // expansion: the parent table of up to kBlock parents (LDS copy): the
+  // work-item prefix, first child / table, degree / token / table size,
+  // node, lookup mode, score and history record
   uint32_t woff[kBlock + 1];
+  uint32_t p_c0[kBlock];
+  uint32_t p_aux[kBlock];
+  uint32_t p_node[kBlock];
+  uint32_t p_hist[kBlock];
+  double p_s[kBlock];
+  uint8_t p_mode[kBlock];
   // selection
   uint32_t hist[256];
   uint32_t wsum[kWaves];
@@ -62,6 +70,12 @@ struct Smem {
 };
 // rank scratch aliases the row arrays (used after expansion only)
 constexpr int kRankChunk = 1024;
+
+// aux word of a hashed parent: log2 of its bucket count, and whether the
+// parent sits at string depth t (then a one-token terminal child closes a
+// key of length t + 1)
+constexpr uint32_t kAuxLog2Mask = 0xFFu;
+constexpr uint32_t kAuxDepthOk = 0x100u;
 
 enum : uint8_t {
   M_NONE = 0,
@@ -299,16 +313,76 @@ __device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
   return (lo < K && sm.row_id[lo] == tok) ? (int)lo : -1;
 }
 
-// Relaxed / acquire / release accesses of the control words (agent scope:
-// the request's workgroups may sit on different XCDs).
+// Data shared between a request's workgroups.  They may sit on different
+// XCDs, whose L2 caches are not coherent with each other, and an agent-scope
+// fence writes back and invalidates the whole L2 of the XCD -- under every
+// other workgroup running there.  So shared data never goes through a fence:
+// it is written with device-coherent stores (write-through, `sc1`) and read
+// by helpers with device-coherent loads; a writer waits for its stores to
+// complete (`vmcnt(0)`: acknowledged at device scope) before it signals, and
+// a reader issues its loads only after it has seen the signal.  The leader,
+// which re-reads the pushes many times during selection, instead invalidates
+// its caches once per step (an acquire fence) and then reads normally.
 __device__ __forceinline__ unsigned long long ld_relaxed(const unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_release(unsigned long long* p, unsigned long long v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint16_t ld_relaxed_u16(const uint16_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_relaxed_f(const float* p) {
+  return __uint_as_float(ld_relaxed((const uint32_t*)p));
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u16(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_f(float* p, float v) {
+  st_dev((uint32_t*)p, __float_as_uint(v));
+}
+__device__ __forceinline__ unsigned long long pack2(uint32_t lo, uint32_t hi) {
+  return (unsigned long long)lo | ((unsigned long long)hi << 32);
+}
+// Records written with device-coherent stores (8 bytes at a time).
+__device__ __forceinline__ void st_next(NextRec* p, uint64_t key, uint32_t node,
+                                        uint32_t jk) {
+  unsigned long long* q = (unsigned long long*)p;
+  st_dev(q, key);
+  st_dev(q + 1, pack2(node, jk));
+}
+__device__ __forceinline__ void st_sel(SelRec* p, const SelRec& r) {
+  unsigned long long* q = (unsigned long long*)p;
+  st_dev(q, (unsigned long long)__double_as_longlong(r.s));
+  st_dev(q + 1, pack2(r.node, r.depth));
+  st_dev(q + 2, pack2(r.phist, r.tok));
+  st_dev(q + 3, pack2(r.jk, r.isnew));
+}
+__device__ __forceinline__ void st_cur(CurRec* p, double s, uint32_t node,
+                                       uint32_t hist) {
+  unsigned long long* q = (unsigned long long*)p;
+  st_dev(q, (unsigned long long)__double_as_longlong(s));
+  st_dev(q + 1, pack2(node, hist));
+}
+__device__ __forceinline__ CurRec ld_cur(const CurRec* p) {
+  const unsigned long long* q = (const unsigned long long*)p;
+  const unsigned long long a = ld_relaxed(q), b = ld_relaxed(q + 1);
+  CurRec r;
+  r.s = __longlong_as_double((long long)a);
+  r.node = (uint32_t)b;
+  r.hist = (uint32_t)(b >> 32);
+  return r;
+}
+// Waits until this wave's stores are complete (acknowledged at device
+// scope); the memory clobber keeps the compiler from moving them past it.
+__device__ __forceinline__ void wait_stores() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Upper bound on spin iterations of a wait (each sleeps ~64 cycles): far
@@ -333,15 +407,33 @@ struct StepView {
   double sent_thr;
 };
 
-// Expands work items [w0, w1): each is (parent, child) for a scanned parent,
-// (parent, proposal) for a searched or hashed parent, or the single pending
-// token of a link parent.  Pushes go to the request's global buffers.
-__device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
-                             uint32_t w1, Smem& sm) {
-  const uint32_t tid = threadIdx.x;
-  const bool lds_woff = v.n_par <= (uint32_t)kBlock;
-  if (lds_woff)
-    for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = v.woff[i];
+// Expands the step's work items: each is (parent, child) for a scanned
+// parent, (parent, proposal) for a searched or hashed parent, or the single
+// pending token of a link parent.  Items go out in chunks of 64 (one per
+// lane of a wave); chunk c belongs to wave c mod nwaves of the request's
+// nwaves waves, so every wave gets an even share of every region of the
+// item space (hashed parents cost a random read per item, scanned ones a
+// coalesced one).  This workgroup's waves are gwave0 .. gwave0 + kWaves - 1.
+// With at most kBlock parents the parent table is read from LDS: the leader
+// has written it there (`par_in_lds`), a helper copies it in first.  Pushes
+// go to the request's global buffers.
+__device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
+                             uint32_t gwave0, uint32_t nwaves, bool par_in_lds,
+                             Smem& sm) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const bool lds_par = v.n_par <= (uint32_t)kBlock;
+  if (lds_par && !par_in_lds) {
+    for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = ld_relaxed(&v.woff[i]);
+    for (uint32_t i = tid; i < v.n_par; i += kBlock) {
+      sm.p_c0[i] = ld_relaxed(&v.pc0[i]);
+      sm.p_aux[i] = ld_relaxed(&v.paux[i]);
+      sm.p_node[i] = ld_relaxed(&v.pnode[i]);
+      sm.p_mode[i] = (uint8_t)ld_relaxed(&v.pmode[i]);
+      const CurRec p = ld_cur(&v.cur[i]);
+      sm.p_s[i] = p.s;
+      sm.p_hist[i] = p.hist;
+    }
+  }
   if (tid == 0) {
     sm.w_children = 0;
     sm.w_probes = 0;
@@ -349,29 +441,39 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
   __syncthreads();
   uint32_t my_children = 0, my_probes = 0;
   const uint32_t K = v.K, t = v.t;
-  for (uint32_t wbase = w0; wbase < w1; wbase += kBlock) {
-    const uint32_t w = wbase + tid;
+  const uint32_t nchunks = (W + 63u) >> 6;
+  for (uint32_t c = gwave0 + (tid >> 6); c < nchunks; c += nwaves) {
+    const uint32_t w = (c << 6) + lane;
     bool do_next = false, do_sel = false;
     uint32_t cnode = 0, pj = 0, k = 0, tok = 0;
     double s2 = 0.0;
-    if (w < w1) {
+    if (w < W) {
       // parent of work item w: the last j with woff[j] <= w
       uint32_t lo = 0, hi = v.n_par;
       while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) >> 1;
-        const uint32_t o = lds_woff ? sm.woff[mid] : v.woff[mid];
+        const uint32_t o = lds_par ? sm.woff[mid] : ld_relaxed(&v.woff[mid]);
         if (o <= w) lo = mid; else hi = mid;
       }
       pj = lo;
-      const uint32_t q = w - (lds_woff ? sm.woff[pj] : v.woff[pj]);
-      const uint32_t md = v.pmode[pj];
-      const uint32_t c0 = v.pc0[pj], aux = v.paux[pj];
+      uint32_t md, c0, aux, q;
+      if (lds_par) {
+        q = w - sm.woff[pj];
+        md = sm.p_mode[pj];
+        c0 = sm.p_c0[pj];
+        aux = sm.p_aux[pj];
+      } else {
+        q = w - ld_relaxed(&v.woff[pj]);
+        md = ld_relaxed(&v.pmode[pj]);
+        c0 = ld_relaxed(&v.pc0[pj]);
+        aux = ld_relaxed(&v.paux[pj]);
+      }
       int pos = -1;
       ft_node_rec cr;
-      bool have_child = false;
+      bool have_child = false, hash_sel = false;
       if (md == M_LP_NEXT || md == M_LP_SEL) {
         pos = row_find(sm, K, aux);
-        cnode = v.pnode[pj];
+        cnode = lds_par ? sm.p_node[pj] : ld_relaxed(&v.pnode[pj]);
       } else if (md == M_SCAN) {
         cnode = c0 + q;
         cr = a.recs[cnode];
@@ -385,7 +487,7 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
         const float x = sm.row_lp[pos];
         k = sm.row_k[pos];
         tok = sm.row_id[pos];
-        const double ps = v.cur[pj].s;
+        const double ps = lds_par ? sm.p_s[pj] : ld_cur(&v.cur[pj]).s;
         // thresholds in double, `<=` drops (louds-trie.cc:87-90)
         const bool low = ((double)x <= (double)v.tok_thr) ||
                          (ps + (double)x <= v.sent_thr);
@@ -408,21 +510,26 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
               }
             }
           } else if (md == M_HASH) {
-            // open addressing in the parent's table
-            const uint32_t mask = (1u << aux) - 1u;
-            const WideSlot* tab = a.wtab + c0;
-            uint32_t sl = fib_slot(tok, aux);
-            for (uint32_t it = 0; it <= mask; ++it) {
-              const WideSlot e = tab[sl];
-              ++my_probes;
-              if (e.tok == tok) {
-                cnode = e.child;
-                cr = a.recs[cnode];
-                have_child = true;
-                break;
+            // both candidate buckets of the cuckoo table, read together
+            const uint32_t lg = aux & kAuxLog2Mask;
+            const uint4* b1 = (const uint4*)(a.wtab + ((uint64_t)c0 + cuckoo_h1(tok, lg)));
+            const uint4* b2 = (const uint4*)(a.wtab + ((uint64_t)c0 + cuckoo_h2(tok, lg)));
+            const uint4 t1 = b1[0], c1 = b1[1], t2 = b2[0], c2 = b2[1];
+            ++my_probes;
+            uint32_t hw = 0, hc = 0;
+            auto chk = [&](uint32_t tw, uint32_t ch) {
+              if (ch != 0u && (tw & kTokMask) == tok) {
+                hw = tw;
+                hc = ch;
               }
-              if (e.tok == kEmpty) break;
-              sl = (sl + 1) & mask;
+            };
+            chk(t1.x, c1.x); chk(t1.y, c1.y); chk(t1.z, c1.z); chk(t1.w, c1.w);
+            chk(t2.x, c2.x); chk(t2.y, c2.y); chk(t2.z, c2.z); chk(t2.w, c2.w);
+            if (hc != 0u) {
+              cnode = hc;
+              have_child = true;
+              // a child one token long, terminal, below a parent at depth t
+              hash_sel = (hw & kSlotSel) && (aux & kAuxDepthOk);
             }
           }
           if (md == M_LP_NEXT) {
@@ -433,8 +540,10 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
             // terminal with |KB| == |Q| -> selected; always next
             // (louds-trie.cc:103-108)
             do_next = true;
-            do_sel = (cr.meta & FT_META_TERMINAL) &&
-                     ((cr.meta & FT_META_DEPTH_MASK) == t + 1);
+            do_sel = (md == M_HASH)
+                         ? hash_sel
+                         : ((cr.meta & FT_META_TERMINAL) &&
+                            (cr.meta & FT_META_DEPTH_MASK) == t + 1);
           }
         }
       }
@@ -442,24 +551,18 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t w0,
     // appends (every lane of the wave reaches these)
     const uint32_t jk = (pj << 16) | k;
     const uint32_t in_ = wave_append(do_next, &v.ctl->n_next);
-    if (do_next && in_ < v.next_cap) {
-      NextRec nr;
-      nr.key = norm_key(s2 * v.lnf_next);
-      nr.node = cnode;
-      nr.jk = jk;
-      v.nextc[in_] = nr;
-    }
+    if (do_next && in_ < v.next_cap) st_next(&v.nextc[in_], norm_key(s2 * v.lnf_next), cnode, jk);
     const uint32_t is_ = wave_append(do_sel, &v.ctl->n_sel);
     if (do_sel && v.nS + is_ < v.sel_cap) {
       SelRec sr;
       sr.s = s2;
       sr.node = cnode;
       sr.depth = t + 1;
-      sr.phist = v.cur[pj].hist;
+      sr.phist = lds_par ? sm.p_hist[pj] : ld_cur(&v.cur[pj]).hist;
       sr.tok = tok;
       sr.jk = jk;
       sr.isnew = 1;
-      v.sel[v.nS + is_] = sr;
+      st_sel(&v.sel[v.nS + is_], sr);
     }
   }
   if (my_children) atomicAdd(&sm.w_children, my_children);
@@ -512,7 +615,6 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
     __syncthreads();
     if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
     seen = v;
-    __threadfence();  // acquire the leader's step data
     const uint32_t t = ld_relaxed(&ctl->t), W = ld_relaxed(&ctl->W);
     StepView sv;
     sv.cur = (const CurRec*)(ws + (ld_relaxed(&ctl->cur_which) ? a.lay.cur1 : a.lay.cur0));
@@ -538,18 +640,15 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
     const float* glp = (const float*)(ws + a.lay.row_lp);
     const uint16_t* gk = (const uint16_t*)(ws + a.lay.row_k);
     for (uint32_t p = tid; p < d.K; p += kBlock) {
-      sm.row_id[p] = gid[p];
-      sm.row_lp[p] = glp[p];
-      sm.row_k[p] = gk[p];
+      sm.row_id[p] = ld_relaxed(&gid[p]);
+      sm.row_lp[p] = ld_relaxed_f(&glp[p]);
+      sm.row_k[p] = ld_relaxed_u16(&gk[p]);
     }
     (void)ids;
     (void)lps;
     __syncthreads();
-    const uint64_t G = a.wgs;
-    const uint32_t w0 = (uint32_t)((uint64_t)W * g / G);
-    const uint32_t w1 = (uint32_t)((uint64_t)W * (g + 1) / G);
-    expand_range(a, sv, w0, w1, sm);
-    __threadfence();  // release this slice's pushes
+    expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, sm);
+    wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
     if (tid == 0) atomicAdd(&ctl->done, 1u);
   }
@@ -615,9 +714,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   uint64_t* step_stats = (uint64_t*)(ob + step_stats_offset(d.F, d.out_T));
   for (uint32_t i = tid; i < d.out_T * kStepStats; i += kBlock) step_stats[i] = 0;
   if (tid == 0) {
-    cur[0].s = 0.0;
-    cur[0].node = 0;
-    cur[0].hist = kNoHist;
+    st_cur(&cur[0], 0.0, 0, kNoHist);
     sm.status = 0;
     sm.cnt_parents = sm.cnt_children = sm.cnt_probes = 0;
   }
@@ -631,11 +728,11 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     const uint32_t ncur0 = n_cur;
     load_row(ids, lps, perm, perm && rowflag[t] != 0, t, K, sm);
     if (tid == 0) {
-      ctl->n_next = 0;
-      ctl->n_sel = 0;
-      ctl->children = 0;
-      ctl->probes = 0;
-      ctl->status = 0;
+      st_dev(&ctl->n_next, 0u);
+      st_dev(&ctl->n_sel, 0u);
+      st_dev(&ctl->children, 0ull);
+      st_dev(&ctl->probes, 0ull);
+      st_dev(&ctl->status, 0u);
     }
     const double lnf_next = lnf[t + 1];
 
@@ -674,8 +771,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
               const WideDir e = a.wdir[sl];
               if (e.node == p.node) {
                 mode = M_HASH;
-                aux = e.log2size;
-                pc0 = e.slot_off;
+                aux = e.log2nb | (sd == t ? kAuxDepthOk : 0u);
+                pc0 = e.bucket_off;
                 break;
               }
               if (e.node == kEmpty) break;
@@ -683,18 +780,30 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             }
           }
         }
-        par_c0[j] = pc0;
-        par_aux[j] = aux;
-        par_node[j] = p.node;
-        par_mode[j] = mode;
+        st_dev(&par_c0[j], pc0);
+        st_dev(&par_aux[j], aux);
+        st_dev(&par_node[j], p.node);
+        st_dev(&par_mode[j], mode);
+        if (n_cur <= (uint32_t)kBlock) {
+          sm.p_c0[j] = pc0;
+          sm.p_aux[j] = aux;
+          sm.p_node[j] = p.node;
+          sm.p_mode[j] = (uint8_t)mode;
+          sm.p_s[j] = p.s;
+          sm.p_hist[j] = p.hist;
+        }
       }
       uint32_t Wc;
       const uint32_t off = block_excl_scan(work, &Wc, sm);
-      if (j < n_cur) par_woff[j] = W + off;
+      if (j < n_cur) {
+        st_dev(&par_woff[j], W + off);
+        if (n_cur <= (uint32_t)kBlock) sm.woff[j] = W + off;
+      }
       W += Wc;
     }
     if (tid == 0) {
-      par_woff[n_cur] = W;
+      st_dev(&par_woff[n_cur], W);
+      if (n_cur <= (uint32_t)kBlock) sm.woff[n_cur] = W;
       sm.cnt_parents += n_cur;
     }
     __syncthreads();
@@ -720,32 +829,30 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     sv.sent_thr = d.sent_thr;
 
     const bool shared = a.wgs > 1 && W >= a.share_min;
-    uint32_t w_end = W;
     if (shared) {
       // publish the row and the step, then wake the helpers
       uint32_t* gid = (uint32_t*)(ws + a.lay.row_id);
       float* glp = (float*)(ws + a.lay.row_lp);
       uint16_t* gk = (uint16_t*)(ws + a.lay.row_k);
       for (uint32_t p = tid; p < K; p += kBlock) {
-        gid[p] = sm.row_id[p];
-        glp[p] = sm.row_lp[p];
-        gk[p] = sm.row_k[p];
+        st_dev(&gid[p], sm.row_id[p]);
+        st_dev_f(&glp[p], sm.row_lp[p]);
+        st_dev_u16(&gk[p], sm.row_k[p]);
       }
       if (tid == 0) {
-        ctl->t = t;
-        ctl->W = W;
-        ctl->n_par = n_cur;
-        ctl->nS = nS;
-        ctl->sel_which = sel_which;
-        ctl->cur_which = cur_which;
-        ctl->done = 0;
+        st_dev(&ctl->t, t);
+        st_dev(&ctl->W, W);
+        st_dev(&ctl->n_par, n_cur);
+        st_dev(&ctl->nS, nS);
+        st_dev(&ctl->sel_which, sel_which);
+        st_dev(&ctl->cur_which, cur_which);
+        st_dev(&ctl->done, 0u);
       }
-      __threadfence();
+      wait_stores();  // the step's data is complete before `go` moves
       __syncthreads();
-      if (tid == 0) st_release(&ctl->go, tag | ++gen);
-      w_end = (uint32_t)((uint64_t)W / a.wgs);
+      if (tid == 0) st_dev(&ctl->go, tag | ++gen);
     }
-    expand_range(a, sv, 0, w_end, sm);
+    expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, sm);
     if (shared) {
       if (tid == 0) {
         for (uint32_t it = 0; it < kSpinLimit; ++it) {
@@ -754,9 +861,11 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         }
         if (ld_relaxed(&ctl->done) < a.wgs - 1) sm.status |= kStatusCorrupt;
       }
-      __syncthreads();
-      __threadfence();  // acquire the helpers' pushes
     }
+    __syncthreads();
+    // the helpers' pushes are complete (they waited for their stores before
+    // counting themselves done): drop stale cached copies before reading
+    if (shared) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const uint32_t n_next = ld_relaxed(&ctl->n_next);
     const uint32_t n_new = ld_relaxed(&ctl->n_sel);
     const unsigned long long w_ch = ld_relaxed(&ctl->children);
@@ -859,7 +968,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       }
       if (b.all && !early_cut) {
         // every push fits: the new items simply become old ones
-        for (uint32_t i = nS + tid; i < nU; i += kBlock) selA[i].isnew = 0;
+        for (uint32_t i = nS + tid; i < nU; i += kBlock) st_dev(&selA[i].isnew, 0u);
         nS = nU;
       } else {
         if (tid == 0) sm.n_out = 0;
@@ -875,7 +984,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
           if (keep && o < sel_cap) {
             SelRec r = selA[i];
             r.isnew = 0;
-            selB[o] = r;
+            st_sel(&selB[o], r);
           }
         }
         __syncthreads();
@@ -924,11 +1033,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       if (keep && o < a.lay.cur_cap && hist_used + o < hist_cap) {
         const uint32_t j = c.jk >> 16, k = c.jk & 0xFFFFu;
         const CurRec p = cur[j];
-        CurRec q;
-        q.s = p.s + (double)lps[(uint64_t)t * K + k];
-        q.node = c.node;
-        q.hist = hist_used + o;
-        cur2[o] = q;
+        st_cur(&cur2[o], p.s + (double)lps[(uint64_t)t * K + k], c.node, hist_used + o);
         HistRec h;
         h.phist = p.hist;
         h.tok = ids[(uint64_t)t * K + k];
@@ -952,7 +1057,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     __syncthreads();
   }
   // release the helpers
-  if (tid == 0) st_release(&ctl->go, tag | kGoExit);
+  if (tid == 0) st_dev(&ctl->go, tag | kGoExit);
 
   // ---- output: selected in ascending (norm, node id) -----------------------
   double* onorm = (double*)(ob + sizeof(OutHeader));
