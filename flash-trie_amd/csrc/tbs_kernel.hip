@@ -42,24 +42,41 @@ namespace ftk {
 
 constexpr int kBlock = 1024;
 constexpr int kWaves = kBlock / 64;
+// selection: bins of the first histogram and the keys one bin may hold in LDS
+constexpr int kWideBits = 11;
+constexpr int kWideBins = 1 << kWideBits;
+constexpr int kBinCap = 2048;
+constexpr int kKeepCap = 4096;
 
 struct Smem {
   // expansion: the current proposal row in ascending token order
   uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
   uint16_t row_k[kMaxLdsTopk];
-  // expansion: the parent table of up to kBlock parents (LDS copy): the
-  // work-item prefix, first child / table, degree / token / table size,
-  // node, lookup mode, score and history record
-  uint32_t woff[kBlock + 1];
-  uint32_t p_c0[kBlock];
-  uint32_t p_aux[kBlock];
-  uint32_t p_node[kBlock];
-  uint32_t p_hist[kBlock];
-  double p_s[kBlock];
-  uint8_t p_mode[kBlock];
+  union {
+    // expansion: the parent table of up to kBlock parents (LDS copy): the
+    // work-item prefix, first child / table, degree / token / table size,
+    // node, lookup mode, score and history record
+    struct {
+      uint32_t woff[kBlock + 1];
+      uint32_t p_c0[kBlock];
+      uint32_t p_aux[kBlock];
+      uint32_t p_node[kBlock];
+      uint32_t p_hist[kBlock];
+      double p_s[kBlock];
+      uint8_t p_mode[kBlock];
+    };
+    // selection: wide histogram and the keys of one histogram bin
+    struct {
+      uint32_t whist[kWideBins];
+      uint64_t bin_key[kBinCap];
+    };
+    // selection: positions of the kept candidates
+    uint32_t keep_idx[kKeepCap];
+  };
   // selection
   uint32_t hist[256];
+  uint64_t red64[2 * kWaves];
   uint32_t wsum[kWaves];
   uint32_t sel_digit, sel_cum, sel_cnt;
   uint32_t n_next, n_sel, n_out, overflow;
@@ -227,6 +244,176 @@ __device__ KeyT radix_kth(uint32_t n, uint32_t need, GetKey gk, Filt filt,
   return prefix;
 }
 
+// Calls f(i, valid, gk(i)) for every item slot i = base + tid of this
+// thread, with four items per thread in flight.
+template <typename GetKey, typename F>
+__device__ __forceinline__ void visit_keys(uint32_t n, GetKey gk, F f) {
+  constexpr uint32_t U = 4;
+  for (uint32_t base = 0; base < n; base += U * kBlock) {
+    uint64_t k[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      k[u] = i < n ? gk(i) : 0;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      f(i, i < n, k[u]);
+    }
+  }
+}
+
+// The `need`-th smallest (1-based) of n 64-bit keys gk(i): one pass for the
+// key range, one histogram pass of
+// kWideBits-bit digits starting at the highest bit in which keys differ,
+// then the keys of the chosen bin are gathered into LDS (if they fit; else
+// another histogram pass narrows the prefix) and the remaining bits are
+// resolved there.  *eq = keys equal to the result, *rem = how many of those
+// are needed to reach `need`.
+template <typename GetKey>
+__device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
+                            uint32_t* eq, uint32_t* rem_out) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // key range
+  uint64_t mn = ~0ull, mx = 0;
+  visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+    if (ok) {
+      mn = min(mn, k);
+      mx = max(mx, k);
+    }
+  });
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    mn = min(mn, (uint64_t)__shfl_xor((unsigned long long)mn, o, 64));
+    mx = max(mx, (uint64_t)__shfl_xor((unsigned long long)mx, o, 64));
+  }
+  if (lane == 0) {
+    sm.red64[wave] = mn;
+    sm.red64[kWaves + wave] = mx;
+  }
+  __syncthreads();
+  mn = sm.red64[0];
+  mx = sm.red64[kWaves];
+  for (int w = 1; w < kWaves; ++w) {
+    mn = min(mn, sm.red64[w]);
+    mx = max(mx, sm.red64[kWaves + w]);
+  }
+  __syncthreads();
+  if (mn == mx) {
+    *eq = n;
+    *rem_out = need;
+    return mn;
+  }
+  // bits above `top` are common to every candidate
+  int top = 63 - __clzll((long long)(mn ^ mx));
+  uint64_t prefix = mn & ~((top >= 63) ? ~0ull : ((2ull << top) - 1ull));
+  uint32_t rem = need;
+  uint32_t cnt = n;
+  for (;;) {
+    // histogram of the kWideBits bits at and below `top`
+    const int sh = top >= kWideBits - 1 ? top - (kWideBits - 1) : 0;
+    const uint32_t nb = 1u << (top - sh + 1);
+    const uint64_t hi_mask = (top >= 63) ? 0ull : ~((2ull << top) - 1ull);
+    for (uint32_t i = tid; i < nb; i += kBlock) sm.whist[i] = 0;
+    __syncthreads();
+    visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+      const bool act = ok && (k & hi_mask) == prefix;
+      hist_add(act, (uint32_t)((k >> sh) & (nb - 1)), sm.whist);
+    });
+    __syncthreads();
+    // the bin holding the rem-th key: each thread owns nb / kBlock bins
+    {
+      const uint32_t per = (nb + kBlock - 1) / kBlock;
+      uint32_t own = 0;
+      for (uint32_t q = 0; q < per; ++q) {
+        const uint32_t b = tid * per + q;
+        if (b < nb) own += sm.whist[b];
+      }
+      uint32_t tot;
+      const uint32_t before = block_excl_scan(own, &tot, sm);
+      if (before < rem && rem <= before + own) {
+        uint32_t c = before;
+        for (uint32_t q = 0; q < per; ++q) {
+          const uint32_t b = tid * per + q;
+          const uint32_t h = sm.whist[b];
+          if (c + h >= rem) {
+            sm.sel_digit = b;
+            sm.sel_cum = c;
+            sm.sel_cnt = h;
+            break;
+          }
+          c += h;
+        }
+      }
+      __syncthreads();
+    }
+    prefix |= (uint64_t)sm.sel_digit << sh;
+    rem -= sm.sel_cum;
+    cnt = sm.sel_cnt;
+    __syncthreads();
+    if (sh == 0) {
+      *eq = cnt;
+      *rem_out = rem;
+      return prefix;
+    }
+    top = sh - 1;
+    if (cnt <= (uint32_t)kBinCap) break;
+  }
+  // gather the keys of the chosen bin, then finish in LDS
+  {
+    const uint64_t hi_mask = ~((2ull << top) - 1ull);
+    if (tid == 0) sm.n_out = 0;
+    __syncthreads();
+    visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+      const bool act = ok && (k & hi_mask) == prefix;
+      const uint32_t o = wave_append(act, &sm.n_out);
+      if (act && o < (uint32_t)kBinCap) sm.bin_key[o] = k;
+    });
+    __syncthreads();
+  }
+  // cnt keys in LDS share the prefix above `top`: 8-bit digits downwards,
+  // until the boundary bin holds one key
+  for (;;) {
+    const int s0 = top >= 7 ? top - 7 : 0;
+    const uint32_t nb = 1u << (top - s0 + 1);
+    const uint64_t msk = ~((2ull << top) - 1ull);
+    for (uint32_t i = tid; i < 256; i += kBlock) sm.hist[i] = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < cnt; i += kBlock) {
+      const uint64_t k = sm.bin_key[i];
+      const bool act = (k & msk) == prefix;
+      hist_add(act, (uint32_t)((k >> s0) & (nb - 1)), sm.hist);
+    }
+    __syncthreads();
+    hist_pick(rem, sm);
+    prefix |= (uint64_t)sm.sel_digit << s0;
+    rem -= sm.sel_cum;
+    const uint32_t c2 = sm.sel_cnt;
+    __syncthreads();
+    if (s0 == 0) {
+      *eq = c2;
+      *rem_out = rem;
+      return prefix;
+    }
+    top = s0 - 1;
+    if (c2 == 1) {
+      // one key left in the bin: it is the answer
+      const uint64_t m2 = ~((2ull << top) - 1ull);
+      for (uint32_t i = tid; i < cnt; i += kBlock) {
+        const uint64_t k = sm.bin_key[i];
+        if ((k & m2) == prefix) sm.red64[0] = k;
+      }
+      __syncthreads();
+      const uint64_t r = sm.red64[0];
+      __syncthreads();
+      *eq = 1;
+      *rem_out = 1;
+      return r;
+    }
+  }
+}
+
 // Thresholds of the bounded-heap emulation (see the file comment).
 struct Bound {
   uint64_t vkey;   // boundary key
@@ -259,9 +446,7 @@ __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
   }
   uint32_t eq, rem;
   // M-th largest key == M-th smallest of ~key
-  const uint64_t nk = radix_kth<uint64_t>(
-      n, M, [&](uint32_t i) { return ~key(i); },
-      [&](uint32_t) { return true; }, sm, &eq, &rem);
+  const uint64_t nk = kth_u64(n, M, [&](uint32_t i) { return ~key(i); }, sm, &eq, &rem);
   b.vkey = ~nk;
   if (eq == rem) return b;  // the whole boundary class fits
   b.tie = 1;
@@ -1021,23 +1206,44 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       __syncthreads();
       break;
     }
-    for (uint32_t base = 0; base < n_next; base += kBlock) {
-      const uint32_t i = base + tid;
-      bool keep = false;
-      NextRec c;
-      if (i < n_next) {
-        c = nextc[i];
-        keep = bound_keep(bn, c.key, bn.tie ? na(i) : 0u, c.node);
-      }
-      const uint32_t o = wave_append(keep, &sm.n_out);
-      if (keep && o < a.lay.cur_cap && hist_used + o < hist_cap) {
-        const uint32_t j = c.jk >> 16, k = c.jk & 0xFFFFu;
-        const CurRec p = cur[j];
-        st_cur(&cur2[o], p.s + (double)lps[(uint64_t)t * K + k], c.node, hist_used + o);
-        HistRec h;
-        h.phist = p.hist;
-        h.tok = ids[(uint64_t)t * K + k];
-        hist[hist_used + o] = h;
+    // survivor i becomes hypothesis o of the next beam
+    auto emit = [&](uint32_t i, uint32_t o) {
+      const NextRec c = nextc[i];
+      const uint32_t j = c.jk >> 16, k = c.jk & 0xFFFFu;
+      const CurRec p = cur[j];
+      st_cur(&cur2[o], p.s + (double)lps[(uint64_t)t * K + k], c.node, hist_used + o);
+      HistRec h;
+      h.phist = p.hist;
+      h.tok = ids[(uint64_t)t * K + k];
+      hist[hist_used + o] = h;
+    };
+    if (keep_cnt <= (uint32_t)kKeepCap) {
+      // positions of the survivors first (from the keys alone; the rest of
+      // a record is read only for a key on the boundary of a cut tie), then
+      // their records: one dependent chain per survivor
+      visit_keys(n_next, nk, [&](uint32_t i, bool ok, uint64_t key) {
+        bool keep = false;
+        if (ok) {
+          if (bn.all || key > bn.vkey) keep = true;
+          else if (key == bn.vkey) keep = bound_keep(bn, key, bn.tie ? na(i) : 0u, nn(i));
+        }
+        const uint32_t o = wave_append(keep, &sm.n_out);
+        if (keep && o < (uint32_t)kKeepCap) sm.keep_idx[o] = i;
+      });
+      __syncthreads();
+      const uint32_t nk2 = min(sm.n_out, (uint32_t)kKeepCap);
+      for (uint32_t o = tid; o < nk2; o += kBlock)
+        if (o < a.lay.cur_cap && hist_used + o < hist_cap) emit(sm.keep_idx[o], o);
+    } else {
+      for (uint32_t base = 0; base < n_next; base += kBlock) {
+        const uint32_t i = base + tid;
+        bool keep = false;
+        if (i < n_next) {
+          const NextRec c = nextc[i];
+          keep = bound_keep(bn, c.key, bn.tie ? na(i) : 0u, c.node);
+        }
+        const uint32_t o = wave_append(keep, &sm.n_out);
+        if (keep && o < a.lay.cur_cap && hist_used + o < hist_cap) emit(i, o);
       }
     }
     __syncthreads();

@@ -291,3 +291,30 @@ def test_shared_steps(ft, po, monkeypatch, wgs, share_min):
                              alpha, early)
                 assert_same_results((got[0][i], got[1][i]), want,
                                     f"wgs {wgs} req {b0 + i} {alpha} {early}")
+
+
+@pytest.mark.parametrize("alpha,early", [(0.0, False), (0.0, True), (5.0, False)])
+def test_wide_tied_selection(ft, po, alpha, early):
+    # 4096 proposals into a 6000-way root with three logp values: thousands
+    # of equal norms share one histogram bin (more than the selection keeps
+    # in LDS), so the boundary is narrowed bit by bit and the arrival-order
+    # rule cuts the tie
+    keys = []
+    for t in range(6000):
+        keys += [[t], [t, t % 3], [t, 1000 + t % 5, t % 7]]
+    rng = np.random.default_rng(11)
+    T, K = 3, 4096
+    ids = np.stack([np.sort(rng.choice(6000, K, replace=False)),
+                    np.arange(K), np.arange(K)]).astype(np.uint32)
+    vals = np.array([-0.5, -1.0, -2.0], dtype=np.float32)
+    lp = vals[rng.choice(3, (T, K), p=[0.01, 0.95, 0.04])]
+    t = _gpu_trie(ft, keys=keys, batch=2, topk=K, steps=T, beams=3000,
+                  inter=16384)
+    o = po.OracleTrie.from_keys(keys)
+    for beams in ([7, 7, 7], [2500, 3000, 40], [3000, 5, 3000]):
+        print("wide tie", alpha, early, beams, flush=True)
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids.tolist()], [lp.tolist()],
+                            -10.0, -40.0, alpha, early)
+        want = o.tbs(beams, ids, lp, -10.0, -40.0, alpha, early)
+        assert_same_results((got[0][0], got[1][0]), want,
+                            f"wide tie {alpha} {early} {beams}")
