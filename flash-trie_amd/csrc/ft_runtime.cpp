@@ -203,14 +203,20 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
           if (i >= ent.size()) break;
           const WideDir& e = ent[i];
           WideBucket* tb = tab.get() + e.bucket_off;
-          std::memset(tb, 0, sizeof(WideBucket) << e.log2nb);
+          for (uint64_t b = 0; b < (1ull << e.log2nb); ++b)
+            for (int sl = 0; sl < 4; ++sl) {
+              tb[b].tok[sl] = kSlotEmptyTok;
+              tb[b].child[sl] = 0;
+            }
           uint64_t rng = 0x9E3779B97F4A7C15ull ^ ((uint64_t)e.node << 1);
           for (uint32_t ch = R[e.node].child_begin; ch < R[e.node + 1].child_begin; ++ch) {
             const uint32_t meta = R[ch].meta;
             const uint32_t elen = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
             const bool sel = (meta & FT_META_TERMINAL) && elen == 1;
             const uint32_t tokw = (R[ch].first_tok & kTokMask) | (sel ? kSlotSel : 0u);
-            if (!cuckoo_insert(tb, e.log2nb, tokw, ch, &rng)) {
+            // tokens that do not fit the slot word: no table for this node
+            if (R[ch].first_tok >= kSlotEmptyTok ||
+                !cuckoo_insert(tb, e.log2nb, tokw, ch, &rng)) {
               failed[i] = 1;
               break;
             }

@@ -88,7 +88,10 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 // buckets, independently, in one memory round trip whatever the table's
 // history of collisions.  A slot's token word carries kSlotSel when the
 // child can close a key one token below its parent (terminal, one-token
-// edge); an empty slot has child 0 (the root is nobody's child).  Tables are
+// edge); an empty slot has child 0 (the root is nobody's child) and token
+// word kSlotEmptyTok, which no stored token equals (a node with a child
+// token >= kSlotEmptyTok gets no table), so a lookup can match token words
+// alone and read the child word of the matching slot only.  Tables are
 // found through a directory keyed by node id (Fibonacci hashing, linear
 // probing, node 0xFFFFFFFF marks an empty entry).
 struct WideDir {
@@ -105,6 +108,7 @@ static_assert(sizeof(WideBucket) == 32, "WideBucket layout");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kSlotSel = 0x80000000u;
 constexpr uint32_t kTokMask = 0x7FFFFFFFu;
+constexpr uint32_t kSlotEmptyTok = 0x7FFFFFFFu;
 __host__ __device__ inline uint32_t fib_slot(uint32_t x, uint32_t log2n) {
   return log2n ? (uint32_t)((x * 0x9E3779B1u) >> (32 - log2n)) : 0u;
 }

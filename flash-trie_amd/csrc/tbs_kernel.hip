@@ -47,6 +47,9 @@ constexpr int kWideBits = 11;
 constexpr int kWideBins = 1 << kWideBits;
 constexpr int kBinCap = 2048;
 constexpr int kKeepCap = 4096;
+// expansion: pushes a workgroup buffers in LDS before one global append
+constexpr int kPushCap = 1024;
+constexpr int kPushSelCap = 256;
 
 struct Smem {
   // expansion: the current proposal row in ascending token order
@@ -74,6 +77,11 @@ struct Smem {
     // selection: positions of the kept candidates
     uint32_t keep_idx[kKeepCap];
   };
+  // expansion: this workgroup's pushes, appended to the request's lists at
+  // the end of its share of the step
+  NextRec push_next[kPushCap];
+  SelRec push_sel[kPushSelCap];
+  uint32_t lq_next, lq_sel, gb_next, gb_sel;
   // selection
   uint32_t hist[256];
   uint64_t red64[2 * kWaves];
@@ -622,6 +630,8 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
   if (tid == 0) {
     sm.w_children = 0;
     sm.w_probes = 0;
+    sm.lq_next = 0;
+    sm.lq_sel = 0;
   }
   __syncthreads();
   uint32_t my_children = 0, my_probes = 0;
@@ -733,29 +743,63 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
         }
       }
     }
-    // appends (every lane of the wave reaches these)
+    // appends (every lane of the wave reaches these): into the LDS
+    // buffers while they have room, the rest straight to the global lists
     const uint32_t jk = (pj << 16) | k;
-    const uint32_t in_ = wave_append(do_next, &v.ctl->n_next);
-    if (do_next && in_ < v.next_cap) st_next(&v.nextc[in_], norm_key(s2 * v.lnf_next), cnode, jk);
-    const uint32_t is_ = wave_append(do_sel, &v.ctl->n_sel);
-    if (do_sel && v.nS + is_ < v.sel_cap) {
-      SelRec sr;
-      sr.s = s2;
-      sr.node = cnode;
-      sr.depth = t + 1;
-      sr.phist = lds_par ? sm.p_hist[pj] : ld_cur(&v.cur[pj]).hist;
-      sr.tok = tok;
-      sr.jk = jk;
-      sr.isnew = 1;
-      st_sel(&v.sel[v.nS + is_], sr);
+    if (__ballot(do_next)) {
+      const uint32_t li = wave_append(do_next, &sm.lq_next);
+      const bool spill = do_next && li >= (uint32_t)kPushCap;
+      const uint32_t gi = wave_append(spill, &v.ctl->n_next);
+      if (do_next) {
+        const uint64_t key = norm_key(s2 * v.lnf_next);
+        if (!spill) {
+          sm.push_next[li].key = key;
+          sm.push_next[li].node = cnode;
+          sm.push_next[li].jk = jk;
+        } else if (gi < v.next_cap) {
+          st_next(&v.nextc[gi], key, cnode, jk);
+        }
+      }
+    }
+    if (__ballot(do_sel)) {
+      const uint32_t li = wave_append(do_sel, &sm.lq_sel);
+      const bool spill = do_sel && li >= (uint32_t)kPushSelCap;
+      const uint32_t gi = wave_append(spill, &v.ctl->n_sel);
+      if (do_sel) {
+        SelRec sr;
+        sr.s = s2;
+        sr.node = cnode;
+        sr.depth = t + 1;
+        sr.phist = lds_par ? sm.p_hist[pj] : ld_cur(&v.cur[pj]).hist;
+        sr.tok = tok;
+        sr.jk = jk;
+        sr.isnew = 1;
+        if (!spill) sm.push_sel[li] = sr;
+        else if (v.nS + gi < v.sel_cap) st_sel(&v.sel[v.nS + gi], sr);
+      }
     }
   }
   if (my_children) atomicAdd(&sm.w_children, my_children);
   if (my_probes) atomicAdd(&sm.w_probes, my_probes);
   __syncthreads();
+  // the buffered pushes: one global append per list
+  const uint32_t nl = min(sm.lq_next, (uint32_t)kPushCap);
+  const uint32_t sl = min(sm.lq_sel, (uint32_t)kPushSelCap);
   if (tid == 0) {
     if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
     if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
+    sm.gb_next = nl ? atomicAdd(&v.ctl->n_next, nl) : 0u;
+    sm.gb_sel = sl ? atomicAdd(&v.ctl->n_sel, sl) : 0u;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < nl; i += kBlock) {
+    const uint32_t o = sm.gb_next + i;
+    const NextRec& r = sm.push_next[i];
+    if (o < v.next_cap) st_next(&v.nextc[o], r.key, r.node, r.jk);
+  }
+  for (uint32_t i = tid; i < sl; i += kBlock) {
+    const uint32_t o = sm.gb_sel + i;
+    if (v.nS + o < v.sel_cap) st_sel(&v.sel[v.nS + o], sm.push_sel[i]);
   }
 }
 
