@@ -609,10 +609,13 @@ struct StepView {
 // coalesced one).  This workgroup's waves are gwave0 .. gwave0 + kWaves - 1.
 // With at most kBlock parents the parent table is read from LDS: the leader
 // has written it there (`par_in_lds`), a helper copies it in first.  Pushes
-// go to the request's global buffers.
+// go to the request's global buffers.  A `solo` workgroup expands the whole
+// step alone: its LDS counters are the list lengths and the control block is
+// not used (the counts stay in sm.lq_next, sm.lq_sel, sm.w_children and
+// sm.w_probes).
 __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
                              uint32_t gwave0, uint32_t nwaves, bool par_in_lds,
-                             Smem& sm) {
+                             bool solo, Smem& sm) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const bool lds_par = v.n_par <= (uint32_t)kBlock;
   if (lds_par && !par_in_lds) {
@@ -749,7 +752,7 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
     if (__ballot(do_next)) {
       const uint32_t li = wave_append(do_next, &sm.lq_next);
       const bool spill = do_next && li >= (uint32_t)kPushCap;
-      const uint32_t gi = wave_append(spill, &v.ctl->n_next);
+      const uint32_t gi = solo ? li : wave_append(spill, &v.ctl->n_next);
       if (do_next) {
         const uint64_t key = norm_key(s2 * v.lnf_next);
         if (!spill) {
@@ -764,7 +767,7 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
     if (__ballot(do_sel)) {
       const uint32_t li = wave_append(do_sel, &sm.lq_sel);
       const bool spill = do_sel && li >= (uint32_t)kPushSelCap;
-      const uint32_t gi = wave_append(spill, &v.ctl->n_sel);
+      const uint32_t gi = solo ? li : wave_append(spill, &v.ctl->n_sel);
       if (do_sel) {
         SelRec sr;
         sr.s = s2;
@@ -786,10 +789,15 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
   const uint32_t nl = min(sm.lq_next, (uint32_t)kPushCap);
   const uint32_t sl = min(sm.lq_sel, (uint32_t)kPushSelCap);
   if (tid == 0) {
-    if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
-    if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
-    sm.gb_next = nl ? atomicAdd(&v.ctl->n_next, nl) : 0u;
-    sm.gb_sel = sl ? atomicAdd(&v.ctl->n_sel, sl) : 0u;
+    if (solo) {
+      sm.gb_next = 0;
+      sm.gb_sel = 0;
+    } else {
+      if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
+      if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
+      sm.gb_next = nl ? atomicAdd(&v.ctl->n_next, nl) : 0u;
+      sm.gb_sel = sl ? atomicAdd(&v.ctl->n_sel, sl) : 0u;
+    }
   }
   __syncthreads();
   for (uint32_t i = tid; i < nl; i += kBlock) {
@@ -876,7 +884,7 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
     (void)ids;
     (void)lps;
     __syncthreads();
-    expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, sm);
+    expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, false, sm);
     wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
     if (tid == 0) atomicAdd(&ctl->done, 1u);
@@ -956,13 +964,6 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     const unsigned long long t0 = wall_clock64();
     const uint32_t ncur0 = n_cur;
     load_row(ids, lps, perm, perm && rowflag[t] != 0, t, K, sm);
-    if (tid == 0) {
-      st_dev(&ctl->n_next, 0u);
-      st_dev(&ctl->n_sel, 0u);
-      st_dev(&ctl->children, 0ull);
-      st_dev(&ctl->probes, 0ull);
-      st_dev(&ctl->status, 0u);
-    }
     const double lnf_next = lnf[t + 1];
 
     // ---- parents: lookup mode, work items, exclusive prefix ---------------
@@ -1069,6 +1070,10 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         st_dev_u16(&gk[p], sm.row_k[p]);
       }
       if (tid == 0) {
+        st_dev(&ctl->n_next, 0u);
+        st_dev(&ctl->n_sel, 0u);
+        st_dev(&ctl->children, 0ull);
+        st_dev(&ctl->probes, 0ull);
         st_dev(&ctl->t, t);
         st_dev(&ctl->W, W);
         st_dev(&ctl->n_par, n_cur);
@@ -1081,7 +1086,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       __syncthreads();
       if (tid == 0) st_dev(&ctl->go, tag | ++gen);
     }
-    expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, sm);
+    expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared, sm);
     if (shared) {
       if (tid == 0) {
         for (uint32_t it = 0; it < kSpinLimit; ++it) {
@@ -1095,10 +1100,10 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // the helpers' pushes are complete (they waited for their stores before
     // counting themselves done): drop stale cached copies before reading
     if (shared) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const uint32_t n_next = ld_relaxed(&ctl->n_next);
-    const uint32_t n_new = ld_relaxed(&ctl->n_sel);
-    const unsigned long long w_ch = ld_relaxed(&ctl->children);
-    const unsigned long long w_pr = ld_relaxed(&ctl->probes);
+    const uint32_t n_next = shared ? ld_relaxed(&ctl->n_next) : sm.lq_next;
+    const uint32_t n_new = shared ? ld_relaxed(&ctl->n_sel) : sm.lq_sel;
+    const unsigned long long w_ch = shared ? ld_relaxed(&ctl->children) : sm.w_children;
+    const unsigned long long w_pr = shared ? ld_relaxed(&ctl->probes) : sm.w_probes;
     __syncthreads();
     n_cands += (uint64_t)n_next + n_new;
     if (tid == 0) {
@@ -1261,7 +1266,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       h.tok = ids[(uint64_t)t * K + k];
       hist[hist_used + o] = h;
     };
-    if (keep_cnt <= (uint32_t)kKeepCap) {
+    if (bn.all) {
+      // everything survives, in push order
+      for (uint32_t i = tid; i < n_next; i += kBlock)
+        if (i < a.lay.cur_cap && hist_used + i < hist_cap) emit(i, i);
+      if (tid == 0) sm.n_out = n_next;
+    } else if (keep_cnt <= (uint32_t)kKeepCap) {
       // positions of the survivors first (from the keys alone; the rest of
       // a record is read only for a key on the boundary of a cut tie), then
       // their records: one dependent chain per survivor
