@@ -76,6 +76,7 @@ struct ft_ctx {
   // wide-node index (device)
   WideDir* d_wdir = nullptr;
   WideBucket* d_wtab = nullptr;
+  uint32_t* d_labels = nullptr;  // per node: first token | kSlotSel
   uint32_t wdir_log2 = 0, wide_min = 0;
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
 
@@ -136,7 +137,7 @@ static bool cuckoo_insert(WideBucket* tb, uint32_t lg, uint32_t tokw,
     const uint32_t tok = tokw & kTokMask;
     const uint32_t b1 = cuckoo_h1(tok, lg), b2 = cuckoo_h2(tok, lg);
     for (const uint32_t b : {b1, b2})
-      for (int sl = 0; sl < 4; ++sl)
+      for (uint32_t sl = 0; sl < kBucketSlots; ++sl)
         if (tb[b].child[sl] == 0) {
           tb[b].tok[sl] = tokw;
           tb[b].child[sl] = child;
@@ -148,11 +149,75 @@ static bool cuckoo_insert(WideBucket* tb, uint32_t lg, uint32_t tokw,
     x ^= x << 17;
     *rng = x;
     const uint32_t b = (x & 1) ? b1 : b2;
-    const int sl = (int)((x >> 1) & 3);
+    const uint32_t sl = (uint32_t)((x >> 1) % kBucketSlots);
     std::swap(tokw, tb[b].tok[sl]);
     std::swap(child, tb[b].child[sl]);
   }
   return false;
+}
+
+// Moves every entry that sits in its second bucket while its first bucket
+// has a free slot into that slot, so that a lookup may stop at a first
+// bucket with a free slot.  Moves only fill first buckets, so it ends.
+static void cuckoo_settle(WideBucket* tb, uint32_t lg) {
+  const uint64_t nb = 1ull << lg;
+  bool moved = true;
+  while (moved) {
+    moved = false;
+    for (uint64_t b = 0; b < nb; ++b)
+      for (uint32_t sl = 0; sl < kBucketSlots; ++sl) {
+        if (tb[b].child[sl] == 0) continue;
+        const uint32_t tok = tb[b].tok[sl] & kTokMask;
+        const uint32_t b1 = cuckoo_h1(tok, lg);
+        if (b1 == b) continue;
+        for (uint32_t s2 = 0; s2 < kBucketSlots; ++s2)
+          if (tb[b1].child[s2] == 0) {
+            tb[b1].tok[s2] = tb[b].tok[sl];
+            tb[b1].child[s2] = tb[b].child[sl];
+            tb[b].tok[sl] = kSlotEmptyTok;
+            tb[b].child[sl] = 0;
+            moved = true;
+            break;
+          }
+      }
+  }
+}
+
+// Per node, its first edge token with kSlotSel when the node can close a
+// key one token below its parent (terminal, one-token edge): what a scan
+// of a parent's children needs, 4 bytes a child.  Uploaded to the device.
+static int build_labels(ft_ctx* c, const uint8_t* image) {
+  const uint64_t N = c->hdr.num_nodes;
+  const ft_node_rec* R = (const ft_node_rec*)(image + c->hdr.recs_offset);
+  std::unique_ptr<uint32_t[]> lab(new (std::nothrow) uint32_t[N]);
+  if (!lab) return fail(FT_E_NOMEM, "labels: host memory");
+  const int T = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::atomic<uint64_t> bad{0};
+  {
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&, w]() {
+        const uint64_t b = N * w / T, e = N * (w + 1) / T;
+        uint64_t nbad = 0;
+        for (uint64_t n = b; n < e; ++n) {
+          const uint32_t meta = R[n].meta;
+          const uint32_t elen = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+          const bool sel = (meta & FT_META_TERMINAL) && elen == 1;
+          if (n > 0 && R[n].first_tok >= kSlotEmptyTok) ++nbad;
+          lab[n] = n == 0 ? kSlotEmptyTok : (R[n].first_tok | (sel ? kSlotSel : 0u));
+        }
+        bad += nbad;
+      });
+    for (auto& x : th) x.join();
+  }
+  if (bad) return fail(FT_E_IMAGE, "ft_create: token ids must be below 2^31 - 1");
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_labels, N * sizeof(uint32_t))) != hipSuccess)
+    return hip_fail(e, "hipMalloc(labels)");
+  if ((e = hipMemcpy(c->d_labels, lab.get(), N * sizeof(uint32_t),
+                     hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy(labels)");
+  return FT_OK;
 }
 
 // Builds the wide-node index on the host (parallel) and uploads it.
@@ -184,7 +249,7 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
     const uint32_t n = nodes[i];
     const uint64_t deg = R[n + 1].child_begin - R[n].child_begin;
     uint32_t lg = 1;
-    while ((2ull << lg) < deg) ++lg;  // 4 slots a bucket, load <= 1/2
+    while (((uint64_t)kBucketSlots << lg) < 2 * deg) ++lg;  // load <= 1/2
     ent[i] = WideDir{n, lg, (uint32_t)buckets, 0};
     buckets += 1ull << lg;
     if (buckets >= 0xFFFFFFF0ull) return fail(FT_E_IMAGE, "wide-node index too large");
@@ -204,7 +269,7 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
           const WideDir& e = ent[i];
           WideBucket* tb = tab.get() + e.bucket_off;
           for (uint64_t b = 0; b < (1ull << e.log2nb); ++b)
-            for (int sl = 0; sl < 4; ++sl) {
+            for (uint32_t sl = 0; sl < kBucketSlots; ++sl) {
               tb[b].tok[sl] = kSlotEmptyTok;
               tb[b].child[sl] = 0;
             }
@@ -221,6 +286,7 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
               break;
             }
           }
+          if (!failed[i]) cuckoo_settle(tb, e.log2nb);
         }
       });
     for (auto& x : th) x.join();
@@ -332,6 +398,10 @@ int ft_create(const void* image, size_t image_bytes, int device,
   }
   c->ring.assign(2 * ft_ctx::kRing, nullptr);
   for (auto& ev : c->ring) (void)hipEventCreate(&ev);
+  if (int rc = build_labels(c, (const uint8_t*)image)) {
+    ft_destroy(c);
+    return rc;
+  }
   if (int rc = build_wide_index(c, (const uint8_t*)image)) {
     ft_destroy(c);
     return rc;
@@ -597,6 +667,7 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   a.epoch = ++c->epoch;
   a.wdir = c->d_wdir;
   a.wtab = c->d_wtab;
+  a.labels = c->d_labels;
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
   (void)hipSetDevice(c->device);
@@ -751,6 +822,7 @@ void ft_destroy(ft_ctx* c) {
   if (c->d_image) (void)hipFree(c->d_image);
   if (c->d_wdir) (void)hipFree(c->d_wdir);
   if (c->d_wtab) (void)hipFree(c->d_wtab);
+  if (c->d_labels) (void)hipFree(c->d_labels);
   for (auto& ev : c->ring)
     if (ev) (void)hipEventDestroy(ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);

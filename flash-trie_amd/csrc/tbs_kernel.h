@@ -83,10 +83,11 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 
 // Wide-node index, built by ft_create from the image: every node with at
 // least `wide_min` children gets a two-choice bucketed cuckoo table
-// token -> child id: 2^log2nb buckets of 4 slots (32 bytes, average load
-// <= 1/2).  A token sits in bucket h1(tok) or h2(tok), so a lookup reads two
-// buckets, independently, in one memory round trip whatever the table's
-// history of collisions.  A slot's token word carries kSlotSel when the
+// token -> child id: 2^log2nb buckets of kBucketSlots slots (64 bytes,
+// average load <= 1/2).  A token sits in bucket h1(tok) or h2(tok), and in
+// h2(tok) only if h1(tok) is full (the build settles entries into their
+// first bucket), so a lookup reads one bucket and reads the second only
+// when the first is full and has no match.  A slot's token word carries kSlotSel when the
 // child can close a key one token below its parent (terminal, one-token
 // edge); an empty slot has child 0 (the root is nobody's child) and token
 // word kSlotEmptyTok, which no stored token equals (a node with a child
@@ -100,11 +101,12 @@ struct WideDir {
   uint32_t bucket_off;  // first bucket of the node's table
   uint32_t pad;
 };
+constexpr uint32_t kBucketSlots = 8;
 struct WideBucket {
-  uint32_t tok[4];
-  uint32_t child[4];
+  uint32_t tok[kBucketSlots];
+  uint32_t child[kBucketSlots];
 };
-static_assert(sizeof(WideBucket) == 32, "WideBucket layout");
+static_assert(sizeof(WideBucket) == 64, "WideBucket layout");
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kSlotSel = 0x80000000u;
 constexpr uint32_t kTokMask = 0x7FFFFFFFu;
@@ -163,6 +165,7 @@ struct KArgs {
   uint32_t scan_limit;
   const WideDir* wdir;   // null: no wide-node index
   const WideBucket* wtab;
+  const uint32_t* labels;  // per node: first token | kSlotSel
   uint32_t wdir_log2;
   uint32_t wide_min;
   uint32_t wgs;        // workgroups per request (1 leader + wgs-1 helpers)

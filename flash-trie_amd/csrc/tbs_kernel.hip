@@ -96,11 +96,11 @@ struct Smem {
 // rank scratch aliases the row arrays (used after expansion only)
 constexpr int kRankChunk = 1024;
 
-// aux word of a hashed parent: log2 of its bucket count, and whether the
-// parent sits at string depth t (then a one-token terminal child closes a
-// key of length t + 1)
-constexpr uint32_t kAuxLog2Mask = 0xFFu;
-constexpr uint32_t kAuxDepthOk = 0x100u;
+// lookup mode word of a parent: the mode, and whether the parent sits at
+// string depth t (only then can a child -- one token long, terminal --
+// close a key of length t + 1)
+constexpr uint32_t kModeMask = 0x7Fu;
+constexpr uint32_t kModeDepthOk = 0x80u;
 
 enum : uint8_t {
   M_NONE = 0,
@@ -666,18 +666,22 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
         c0 = ld_relaxed(&v.pc0[pj]);
         aux = ld_relaxed(&v.paux[pj]);
       }
+      const bool depth_ok = (md & kModeDepthOk) != 0;
+      md &= kModeMask;
       int pos = -1;
       ft_node_rec cr;
-      bool have_child = false, hash_sel = false;
+      bool have_child = false, label_sel = false;
       if (md == M_LP_NEXT || md == M_LP_SEL) {
         pos = row_find(sm, K, aux);
         cnode = lds_par ? sm.p_node[pj] : ld_relaxed(&v.pnode[pj]);
       } else if (md == M_SCAN) {
+        // the child's label: its first token, and whether it closes a key
         cnode = c0 + q;
-        cr = a.recs[cnode];
+        const uint32_t lw = a.labels[cnode];
         ++my_children;
-        pos = row_find(sm, K, cr.first_tok);
+        pos = row_find(sm, K, lw & kTokMask);
         have_child = true;
+        label_sel = (lw & kSlotSel) && depth_ok;
       } else if (md == M_SEARCH || md == M_HASH) {
         pos = (int)q;
       }
@@ -708,26 +712,35 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
               }
             }
           } else if (md == M_HASH) {
-            // both candidate buckets of the cuckoo table, read together
-            const uint32_t lg = aux & kAuxLog2Mask;
-            const uint4* b1 = (const uint4*)(a.wtab + ((uint64_t)c0 + cuckoo_h1(tok, lg)));
-            const uint4* b2 = (const uint4*)(a.wtab + ((uint64_t)c0 + cuckoo_h2(tok, lg)));
-            const uint4 t1 = b1[0], c1 = b1[1], t2 = b2[0], c2 = b2[1];
-            ++my_probes;
+            // the token's first cuckoo bucket, and its second only when the
+            // first is full without a match
+            const uint32_t lg = aux;
+            uint32_t b = c0 + cuckoo_h1(tok, lg);
             uint32_t hw = 0, hc = 0;
-            auto chk = [&](uint32_t tw, uint32_t ch) {
-              if (ch != 0u && (tw & kTokMask) == tok) {
-                hw = tw;
-                hc = ch;
+            for (int round = 0; round < 2; ++round) {
+              const uint4* tw4 = (const uint4*)a.wtab[b].tok;
+              const uint4 ta = tw4[0], tb = tw4[1];
+              ++my_probes;
+              const uint32_t tw[8] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y, tb.z, tb.w};
+              int hs = -1;
+              bool full = true;
+#pragma unroll
+              for (int sl = 0; sl < 8; ++sl) {
+                if ((tw[sl] & kTokMask) == tok) hs = sl;
+                full = full && tw[sl] != kSlotEmptyTok;
               }
-            };
-            chk(t1.x, c1.x); chk(t1.y, c1.y); chk(t1.z, c1.z); chk(t1.w, c1.w);
-            chk(t2.x, c2.x); chk(t2.y, c2.y); chk(t2.z, c2.z); chk(t2.w, c2.w);
+              if (hs >= 0) {
+                hw = tw[hs];
+                hc = a.wtab[b].child[hs];
+                break;
+              }
+              if (!full) break;
+              b = c0 + cuckoo_h2(tok, lg);
+            }
             if (hc != 0u) {
               cnode = hc;
               have_child = true;
-              // a child one token long, terminal, below a parent at depth t
-              hash_sel = (hw & kSlotSel) && (aux & kAuxDepthOk);
+              label_sel = (hw & kSlotSel) && depth_ok;
             }
           }
           if (md == M_LP_NEXT) {
@@ -738,10 +751,10 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
             // terminal with |KB| == |Q| -> selected; always next
             // (louds-trie.cc:103-108)
             do_next = true;
-            do_sel = (md == M_HASH)
-                         ? hash_sel
-                         : ((cr.meta & FT_META_TERMINAL) &&
-                            (cr.meta & FT_META_DEPTH_MASK) == t + 1);
+            do_sel = (md == M_SEARCH)
+                         ? ((cr.meta & FT_META_TERMINAL) &&
+                            (cr.meta & FT_META_DEPTH_MASK) == t + 1)
+                         : label_sel;
           }
         }
       }
@@ -1001,7 +1014,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
               const WideDir e = a.wdir[sl];
               if (e.node == p.node) {
                 mode = M_HASH;
-                aux = e.log2nb | (sd == t ? kAuxDepthOk : 0u);
+                aux = e.log2nb;
                 pc0 = e.bucket_off;
                 break;
               }
@@ -1010,6 +1023,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             }
           }
         }
+        if ((mode == M_SCAN || mode == M_HASH) && sd == t) mode |= kModeDepthOk;
         st_dev(&par_c0[j], pc0);
         st_dev(&par_aux[j], aux);
         st_dev(&par_node[j], p.node);
