@@ -718,23 +718,22 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
             uint32_t b = c0 + cuckoo_h1(tok, lg);
             uint32_t hw = 0, hc = 0;
             for (int round = 0; round < 2; ++round) {
-              const uint4* tw4 = (const uint4*)a.wtab[b].tok;
-              const uint4 ta = tw4[0], tb = tw4[1];
+              // the whole bucket (tokens and children) in one read
+              const uint4* bw = (const uint4*)&a.wtab[b];
+              const uint4 ta = bw[0], tb = bw[1], ca = bw[2], cb = bw[3];
               ++my_probes;
               const uint32_t tw[8] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y, tb.z, tb.w};
-              int hs = -1;
+              const uint32_t cw[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
               bool full = true;
 #pragma unroll
               for (int sl = 0; sl < 8; ++sl) {
-                if ((tw[sl] & kTokMask) == tok) hs = sl;
+                if ((tw[sl] & kTokMask) == tok) {
+                  hw = tw[sl];
+                  hc = cw[sl];
+                }
                 full = full && tw[sl] != kSlotEmptyTok;
               }
-              if (hs >= 0) {
-                hw = tw[hs];
-                hc = a.wtab[b].child[hs];
-                break;
-              }
-              if (!full) break;
+              if (hc != 0u || !full) break;
               b = c0 + cuckoo_h2(tok, lg);
             }
             if (hc != 0u) {
