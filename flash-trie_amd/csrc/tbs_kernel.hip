@@ -1,9 +1,10 @@
 // tbs_kernel.hip -- trie beam search (TBS) kernel for gfx950 (MI355X).
 //
-// One persistent workgroup of 1024 threads (16 wave64) runs the complete
-// search of one request: every decoding step's expansion, validation and
-// pruning, with the whole batch in a single cooperative launch and no host
-// round trip between steps.  Semantics are those of the reference CPU path
+// The whole batch is one cooperative launch with no host round trip between
+// decoding steps.  Each request has a leader workgroup of 1024 threads (16
+// wave64) that runs every step -- parent table, expansion, validation,
+// pruning -- and helper workgroups that join the expansion of the steps
+// with many work items.  Semantics are those of the reference CPU path
 // LoudsTrie::tbs (lib/marisa/grimoire/trie/louds-trie.cc:75-177):
 //
 //  * cur is processed parent by parent in ascending (norm, node id) order and
