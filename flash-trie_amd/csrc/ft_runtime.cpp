@@ -84,7 +84,8 @@ struct ft_ctx {
   uint64_t out_stride = 0;
   bool launched = false;
   uint32_t scan_mult = 8;
-  uint32_t wgs_req = 64;      // workgroups per request (clamped to residency)
+  uint32_t wgs_req = 4096;    // workgroups per request (clamped to residency:
+                              // a lone request gets every CU)
   uint32_t share_min = 8192;  // work items from which a step is shared
   int max_resident = 0;
   uint32_t epoch = 0;
