@@ -40,7 +40,10 @@ METRIC = "mean/p99 trie-search ms @800M keys, beam 1000; peak q/s over batch 1-8
 HBM_PEAK_GBS = 8000.0
 PUBLISHED_PEAK_QPS = 1539.0  # A100, beam 1000, batch 8 (README.md:64)
 
-TOK_THR, SENT_THR, ALPHA = -10.0, -40.0, 5.0
+ALPHA = 5.0
+# per workload: token / sentence log-prob thresholds and early exit
+RULES = {"paper": (-10.0, -40.0, False), "c2": (-10.0, -40.0, False),
+         "stress": (-4.0, -20.0, True)}
 
 
 def log(*a):
@@ -53,7 +56,7 @@ def parse():
     p.add_argument("--steps", type=int, default=400,
                    help="timed launches per batch size")
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", default="paper", choices=["c2", "paper"])
+    p.add_argument("--config", default="paper", choices=["c2", "paper", "stress"])
     p.add_argument("--beam", type=int, default=1000)
     p.add_argument("--pool", type=int, default=512,
                    help="distinct requests staged in HBM")
@@ -62,6 +65,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--boundary", type=int, default=100,
                    help="batch-1 requests timed through the C++ boundary")
+    p.add_argument("--beam-sweep", default="100,500",
+                   help="other beam widths (K = beam) timed at batch 1 "
+                        "(paper workload; empty to skip)")
     return p.parse_args()
 
 
@@ -91,6 +97,15 @@ def build_workload(ft, cfg, beam):
         trie.build_arrays(toks, offs)
         del toks, offs
         desc = "10M-key trie, 256k vocab, key length 4-12, Zipf(1.1)"
+    elif cfg == "stress":
+        vocab, steps = 2_200_000, 32
+        trie = ft.Trie()
+        os.environ["FT_SYNTH_VERBOSE"] = "1"
+        ft.synth_paper_trie(trie, 200_000_000, vocab, 1.05, 1, lmin=16,
+                            lmax=32, p_end=0.25)
+        desc = ("stress: 200M-key trie, 2.2M vocab (heavy-fanout root), key "
+                "length 16-32, Zipf(1.05) prefix sharing; early exit, "
+                "thresholds -4 / -20")
     else:
         vocab, steps = 2_200_000, 16
         trie = ft.Trie()
@@ -101,6 +116,45 @@ def build_workload(ft, cfg, beam):
     log(f"trie: {trie.num_keys()} keys, {trie.num_nodes()} nodes, "
         f"{trie.total_size() / 2**30:.2f} GiB image, {time.time() - t0:.1f}s")
     return trie, vocab, steps, desc
+
+
+def beam_sweep(ft, trie, vocab, T, widths, steps, warmup, rules, ot=None):
+    """Batch-1 kernel latency at other beam widths (K = beam, as many seed
+    paths), each over its own pool of seeded requests; spot-checked against
+    the oracle when it is given."""
+    tok_thr, sent_thr, early = rules
+    out = {}
+    for B in widths:
+        P = 64
+        ids, lp = ft.synth_requests(trie, 1000 + B, P, vocab, T, B, B, 0.3, 2.5,
+                                    True, 0, model=1)
+        beams = np.full((P, T), B, dtype=np.uint32)
+        ft.stage(trie, beams, ids, lp, tok_thr, sent_thr, ALPHA, early)
+        for i in range(warmup):
+            ft.launch(trie, i % P, 1)
+        ft.sync(trie)
+        for i in range(steps):
+            ft.launch(trie, i % P, 1)
+        ms = ft.launch_times(trie, min(steps, 1024))
+        res = {"mean": round(float(ms.mean()), 4),
+               "p99": round(float(np.percentile(ms, 99)), 4)}
+        if ot is not None:
+            for first in range(0, P):
+                ft.launch(trie, first, 1)
+            ft.sync(trie)
+            cnt, norms, lens, toks, _ = ft.fetch(trie)
+            bad = 0
+            for r in range(4):
+                s_, n_ = ot.tbs(beams[r], ids[r], lp[r], tok_thr, sent_thr,
+                                ALPHA, early)
+                c = int(cnt[r])
+                g = [toks[r, j, :lens[r, j]].tolist() for j in range(c)]
+                bad += int(g != s_ or not np.array_equal(norms[r, :c], n_))
+            res["parity"] = {"checked": 4, "mismatches": bad}
+        out[str(B)] = res
+        log(f"beam {B}: batch-1 kernel mean {res['mean']:.3f} ms p99 "
+            f"{res['p99']:.3f} ms")
+    return out
 
 
 def main():
@@ -116,6 +170,7 @@ def main():
     import flashtrie as ft
 
     B = K = args.beam
+    TOK_THR, SENT_THR, EARLY = RULES[args.config]
     trie, vocab, T, desc = build_workload(ft, args.config, B)
     batches = [int(x) for x in args.batches.split(",")]
     P = args.pool
@@ -131,7 +186,7 @@ def main():
     ft.reserve_staging(trie, P)
     info = trie.device_info()
     log("device", info)
-    ft.stage(trie, beams, ids, lp, TOK_THR, SENT_THR, ALPHA, False)
+    ft.stage(trie, beams, ids, lp, TOK_THR, SENT_THR, ALPHA, EARLY)
     ft.launch(trie, 0, 1)
     ft.sync(trie)
 
@@ -192,7 +247,7 @@ def main():
     for r in range(nbd):
         t0 = time.perf_counter()
         ft.stage(trie, beams[r:r + 1], ids[r:r + 1], lp[r:r + 1], TOK_THR,
-                 SENT_THR, ALPHA, False)
+                 SENT_THR, ALPHA, EARLY)
         ft.launch(trie)
         c1, n1, l1, t1, _ = ft.fetch(trie)
         bl.append((time.perf_counter() - t0) * 1e3)
@@ -227,7 +282,7 @@ def main():
                 if r >= P:
                     return
                 s, n, w = ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR,
-                                 ALPHA, False, with_work=True)
+                                 ALPHA, EARLY, with_work=True)
                 with lock:
                     done.append((r, s, n))
                     works.append(w)
@@ -243,7 +298,7 @@ def main():
         lat1 = []
         for r in range(3):
             t1 = time.perf_counter()
-            ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, False)
+            ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, EARLY)
             lat1.append((time.perf_counter() - t1) * 1e3)
         # the as-written linear sibling scan costs O(K x degree) per parent:
         # ~2e9 label reads at the 2.2M-child root of the paper trie, so it
@@ -252,7 +307,7 @@ def main():
         if args.config == "c2":
             for r in range(2):
                 t1 = time.perf_counter()
-                ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, False,
+                ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, EARLY,
                        variant=pyoracle.AS_WRITTEN)
                 aw.append((time.perf_counter() - t1) * 1e3)
         aw_txt = (f"{np.mean(aw):.1f} ms/request" if aw else
@@ -290,6 +345,15 @@ def main():
     else:
         wstats = {}
 
+    # ---- other beam widths at batch 1 (after everything that reads the
+    # staged pool) ------------------------------------------------------------
+    by_beam = {}
+    widths = [int(x) for x in args.beam_sweep.split(",") if x.strip()]
+    if args.config == "paper" and widths:
+        by_beam = beam_sweep(ft, trie, vocab, T, [w for w in widths if w <= B],
+                             min(args.steps, 300), args.warmup,
+                             RULES[args.config], None if args.no_cpu else ot)
+
     kb = kern_ms[peak_b]
     roof = None
     if algo_bytes is not None:
@@ -321,13 +385,17 @@ def main():
                    "proposals": "example row model: seed-path tokens "
                                 "U(-2.2,-0.2), distractors U(-12,-4), "
                                 f"{B} seed paths",
-                   "thresholds": [TOK_THR, SENT_THR], "length_norm": ALPHA},
+                   "thresholds": [TOK_THR, SENT_THR], "length_norm": ALPHA,
+                   "early_exit": EARLY},
         "latency_ms": {"mean": round(float(k1.mean()), 4),
                        "p99": round(float(np.percentile(k1, 99)), 4),
                        "boundary_mean": (round(float(bl.mean()), 4)
                                          if bl.size else None),
                        "boundary_p99": (round(float(np.percentile(bl, 99)), 4)
                                         if bl.size else None)},
+        "latency_ms_by_beam": dict(
+            by_beam, **{str(B): {"mean": round(float(kern_ms.get(1, kb).mean()), 4),
+                                 "p99": round(float(np.percentile(kern_ms.get(1, kb), 99)), 4)}}),
         "qps_by_batch": {str(b): round(v, 1) for b, v in qps.items()},
         "kernel_ms_by_batch": {str(b): round(float(v.mean()), 4)
                                for b, v in kern_ms.items()},

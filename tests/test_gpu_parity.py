@@ -318,3 +318,30 @@ def test_wide_tied_selection(ft, po, alpha, early):
         want = o.tbs(beams, ids, lp, -10.0, -40.0, alpha, early)
         assert_same_results((got[0][0], got[1][0]), want,
                             f"wide tie {alpha} {early} {beams}")
+
+
+@pytest.mark.parametrize("early", [True, False])
+def test_stress_long_keys_tight_thresholds(ft, po, early):
+    # the stress shape at small scale: long keys (16-32 tokens), 32 steps,
+    # tight thresholds (token -4, sentence -20) that reject most candidates,
+    # early exit on and off, a batch of 8 in one launch
+    toks, offs = ft.synth_keys(60000, 8192, 16, 32, 1.1, 12)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=8, topk=64, steps=32,
+                  beams=48, inter=1 << 16)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 16, 8192, 32, 64, 48, 0.3, 2.0, True, 12,
+                                model=1)
+    # a final beam of 3: early exit cuts `selected` at its third push
+    beams = [48] * 31 + [3]
+    for b0 in range(0, 16, 8):
+        print("stress batch", b0, early, flush=True)
+        got = ft.bs_tbs_gpu(t, 8, [beams] * 8,
+                            [ids[b0 + i].tolist() for i in range(8)],
+                            [lp[b0 + i].tolist() for i in range(8)],
+                            -4.0, -20.0, 5.0, early)
+        for i in range(8):
+            want = o.tbs(beams, ids[b0 + i], lp[b0 + i], -4.0, -20.0, 5.0,
+                         early)
+            assert_same_results((got[0][i], got[1][i]), want,
+                                f"stress req {b0 + i} early={early}")
+        assert any(len(s) for s in got[0]), "every stress request came back empty"
