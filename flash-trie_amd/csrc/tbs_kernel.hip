@@ -86,6 +86,8 @@ struct Smem {
   // selection
   uint32_t hist[256];
   uint64_t red64[2 * kWaves];
+  double redd[4][kWaves];
+  unsigned long long nk_lo, nk_hi;  // bounds of the step's next-list keys
   uint32_t wsum[kWaves];
   uint32_t sel_digit, sel_cum, sel_cnt;
   uint32_t n_next, n_sel, n_out, overflow;
@@ -282,33 +284,38 @@ __device__ __forceinline__ void visit_keys(uint32_t n, GetKey gk, F f) {
 // are needed to reach `need`.
 template <typename GetKey>
 __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
-                            uint32_t* eq, uint32_t* rem_out) {
+                            uint32_t* eq, uint32_t* rem_out, bool have_range,
+                            uint64_t rmin, uint64_t rmax) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  // key range
-  uint64_t mn = ~0ull, mx = 0;
-  visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
-    if (ok) {
-      mn = min(mn, k);
-      mx = max(mx, k);
-    }
-  });
+  // key range: given (bounds of every key), or one pass
+  uint64_t mn = rmin, mx = rmax;
+  if (!have_range) {
+    mn = ~0ull;
+    mx = 0;
+    visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+      if (ok) {
+        mn = min(mn, k);
+        mx = max(mx, k);
+      }
+    });
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    mn = min(mn, (uint64_t)__shfl_xor((unsigned long long)mn, o, 64));
-    mx = max(mx, (uint64_t)__shfl_xor((unsigned long long)mx, o, 64));
+    for (int o = 32; o >= 1; o >>= 1) {
+      mn = min(mn, (uint64_t)__shfl_xor((unsigned long long)mn, o, 64));
+      mx = max(mx, (uint64_t)__shfl_xor((unsigned long long)mx, o, 64));
+    }
+    if (lane == 0) {
+      sm.red64[wave] = mn;
+      sm.red64[kWaves + wave] = mx;
+    }
+    __syncthreads();
+    mn = sm.red64[0];
+    mx = sm.red64[kWaves];
+    for (int w = 1; w < kWaves; ++w) {
+      mn = min(mn, sm.red64[w]);
+      mx = max(mx, sm.red64[kWaves + w]);
+    }
+    __syncthreads();
   }
-  if (lane == 0) {
-    sm.red64[wave] = mn;
-    sm.red64[kWaves + wave] = mx;
-  }
-  __syncthreads();
-  mn = sm.red64[0];
-  mx = sm.red64[kWaves];
-  for (int w = 1; w < kWaves; ++w) {
-    mn = min(mn, sm.red64[w]);
-    mx = max(mx, sm.red64[kWaves + w]);
-  }
-  __syncthreads();
   if (mn == mx) {
     *eq = n;
     *rem_out = need;
@@ -444,10 +451,12 @@ __device__ __forceinline__ bool bound_keep(const Bound& b, uint64_t key,
 // Bounded heap of capacity M over n items (see the file comment).  key(i),
 // arr(i) and node(i) read the items; arr() is only called on the tie path,
 // after `need_ranks()` has made parent ranks available.
+// With `have_range`, every key(i) lies in [kmin, kmax].
 template <typename GetKey, typename GetArr, typename GetNode, typename Ranks>
 __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
                                 GetArr arr, GetNode node, Ranks need_ranks,
-                                Smem& sm) {
+                                Smem& sm, bool have_range = false,
+                                uint64_t kmin = 0, uint64_t kmax = ~0ull) {
   Bound b{0, 0, 0, 0, 0};
   if (n <= M) {
     b.all = 1;
@@ -455,7 +464,8 @@ __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
   }
   uint32_t eq, rem;
   // M-th largest key == M-th smallest of ~key
-  const uint64_t nk = kth_u64(n, M, [&](uint32_t i) { return ~key(i); }, sm, &eq, &rem);
+  const uint64_t nk = kth_u64(n, M, [&](uint32_t i) { return ~key(i); }, sm, &eq,
+                              &rem, have_range, ~kmax, ~kmin);
   b.vkey = ~nk;
   if (eq == rem) return b;  // the whole boundary class fits
   b.tie = 1;
@@ -1141,6 +1151,51 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       row[7] = w_pr;
     }
 
+    // ---- bounds of the next-list keys, from LDS ----------------------------
+    // A push's score is a parent score plus a proposal logp and its key a
+    // monotone function of the score (rounding is monotone too), so the
+    // extreme parent scores and logps bound every key: the selection needs
+    // no pass over the list for its range.
+    const uint32_t Mnext = beams[t];
+    const bool next_range = n_next > Mnext && n_cur <= (uint32_t)kBlock;
+    if (next_range) {
+      double smin = __builtin_huge_val(), smax = -__builtin_huge_val();
+      double xmin = __builtin_huge_val(), xmax = -__builtin_huge_val();
+      for (uint32_t j = tid; j < n_cur; j += kBlock) {
+        smin = min(smin, sm.p_s[j]);
+        smax = max(smax, sm.p_s[j]);
+      }
+      for (uint32_t p = tid; p < K; p += kBlock) {
+        xmin = min(xmin, (double)sm.row_lp[p]);
+        xmax = max(xmax, (double)sm.row_lp[p]);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        smin = min(smin, __shfl_xor(smin, o, 64));
+        smax = max(smax, __shfl_xor(smax, o, 64));
+        xmin = min(xmin, __shfl_xor(xmin, o, 64));
+        xmax = max(xmax, __shfl_xor(xmax, o, 64));
+      }
+      if ((tid & 63u) == 0) {
+        sm.redd[0][tid >> 6] = smin;
+        sm.redd[1][tid >> 6] = smax;
+        sm.redd[2][tid >> 6] = xmin;
+        sm.redd[3][tid >> 6] = xmax;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        for (int w = 1; w < kWaves; ++w) {
+          smin = min(smin, sm.redd[0][w]);
+          smax = max(smax, sm.redd[1][w]);
+          xmin = min(xmin, sm.redd[2][w]);
+          xmax = max(xmax, sm.redd[3][w]);
+        }
+        sm.nk_lo = norm_key((smin + xmin) * lnf_next);
+        sm.nk_hi = norm_key((smax + xmax) * lnf_next);
+      }
+      __syncthreads();
+    }
+
     // ---- parent ranks (only when arrival order is needed) ---------------
     bool ranks_done = false;
     const double lnf_cur = lnf[t];
@@ -1253,14 +1308,15 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
 
     // ---- next --------------------------------------------------------------
-    const uint32_t M = beams[t];
+    const uint32_t M = Mnext;
     auto nk = [&](uint32_t i) { return nextc[i].key; };
     auto na = [&](uint32_t i) {
       const uint32_t jk = nextc[i].jk;
       return rank[jk >> 16] * K + (jk & 0xFFFFu);
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
-    const Bound bn = bounded_select(n_next, M, nk, na, nn, compute_ranks, sm);
+    const Bound bn = bounded_select(n_next, M, nk, na, nn, compute_ranks, sm,
+                                    next_range, sm.nk_lo, sm.nk_hi);
     if (tid == 0) sm.n_out = 0;
     __syncthreads();
     const uint32_t keep_cnt = bn.all ? n_next : M;
