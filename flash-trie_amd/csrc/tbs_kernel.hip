@@ -70,13 +70,15 @@ struct Smem {
       double p_s[kBlock];
       uint8_t p_mode[kBlock];
     };
-    // selection: wide histogram and the keys of one histogram bin
+    // selection: positions of the kept candidates, and the keys and
+    // positions of one histogram bin
     struct {
-      uint32_t whist[kWideBins];
+      uint32_t keep_idx[kKeepCap];
       uint64_t bin_key[kBinCap];
+      uint32_t bin_idx[kBinCap];
     };
-    // selection: positions of the kept candidates
-    uint32_t keep_idx[kKeepCap];
+    // selection: wide histogram (done before keep_idx is filled)
+    uint32_t whist[kWideBins];
   };
   // expansion: this workgroup's pushes, appended to the request's lists at
   // the end of its share of the step
@@ -90,6 +92,7 @@ struct Smem {
   unsigned long long nk_lo, nk_hi;  // bounds of the step's next-list keys
   uint32_t wsum[kWaves];
   uint32_t sel_digit, sel_cum, sel_cnt;
+  uint32_t n_keep, collected;
   uint32_t n_next, n_sel, n_out, overflow;
   uint32_t status;
   unsigned long long cnt_parents, cnt_children, cnt_probes;
@@ -282,11 +285,17 @@ __device__ __forceinline__ void visit_keys(uint32_t n, GetKey gk, F f) {
 // another histogram pass narrows the prefix) and the remaining bits are
 // resolved there.  *eq = keys equal to the result, *rem = how many of those
 // are needed to reach `need`.
+//
+// With `collect`, the gather pass also lists, in sm.keep_idx, the items in
+// bins below the chosen one (sm.n_keep of them) and keeps the chosen bin's
+// positions in sm.bin_idx, and sm.collected says that it ran: then a bounded
+// selection needs no further pass over the list.
 template <typename GetKey>
 __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
                             uint32_t* eq, uint32_t* rem_out, bool have_range,
-                            uint64_t rmin, uint64_t rmax) {
+                            uint64_t rmin, uint64_t rmax, bool collect = false) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  if (tid == 0) sm.collected = 0;
   // key range: given (bounds of every key), or one pass
   uint64_t mn = rmin, mx = rmax;
   if (!have_range) {
@@ -379,12 +388,25 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
   // gather the keys of the chosen bin, then finish in LDS
   {
     const uint64_t hi_mask = ~((2ull << top) - 1ull);
-    if (tid == 0) sm.n_out = 0;
+    if (tid == 0) {
+      sm.n_out = 0;
+      sm.n_keep = 0;
+      sm.collected = collect ? 1u : 0u;
+    }
     __syncthreads();
-    visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
-      const bool act = ok && (k & hi_mask) == prefix;
+    visit_keys(n, gk, [&](uint32_t i, bool ok, uint64_t k) {
+      const uint64_t hk = k & hi_mask;
+      const bool act = ok && hk == prefix;
       const uint32_t o = wave_append(act, &sm.n_out);
-      if (act && o < (uint32_t)kBinCap) sm.bin_key[o] = k;
+      if (act && o < (uint32_t)kBinCap) {
+        sm.bin_key[o] = k;
+        sm.bin_idx[o] = i;
+      }
+      if (collect) {
+        const bool below = ok && hk < prefix;
+        const uint32_t q = wave_append(below, &sm.n_keep);
+        if (below && q < (uint32_t)kKeepCap) sm.keep_idx[q] = i;
+      }
     });
     __syncthreads();
   }
@@ -451,12 +473,14 @@ __device__ __forceinline__ bool bound_keep(const Bound& b, uint64_t key,
 // Bounded heap of capacity M over n items (see the file comment).  key(i),
 // arr(i) and node(i) read the items; arr() is only called on the tie path,
 // after `need_ranks()` has made parent ranks available.
-// With `have_range`, every key(i) lies in [kmin, kmax].
+// With `have_range`, every key(i) lies in [kmin, kmax].  With `collect`,
+// see kth_u64 (the items with a key above the boundary bin are listed).
 template <typename GetKey, typename GetArr, typename GetNode, typename Ranks>
 __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
                                 GetArr arr, GetNode node, Ranks need_ranks,
                                 Smem& sm, bool have_range = false,
-                                uint64_t kmin = 0, uint64_t kmax = ~0ull) {
+                                uint64_t kmin = 0, uint64_t kmax = ~0ull,
+                                bool collect = false) {
   Bound b{0, 0, 0, 0, 0};
   if (n <= M) {
     b.all = 1;
@@ -465,7 +489,7 @@ __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
   uint32_t eq, rem;
   // M-th largest key == M-th smallest of ~key
   const uint64_t nk = kth_u64(n, M, [&](uint32_t i) { return ~key(i); }, sm, &eq,
-                              &rem, have_range, ~kmax, ~kmin);
+                              &rem, have_range, ~kmax, ~kmin, collect);
   b.vkey = ~nk;
   if (eq == rem) return b;  // the whole boundary class fits
   b.tie = 1;
@@ -1315,8 +1339,15 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       return rank[jk >> 16] * K + (jk & 0xFFFFu);
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
+    const bool collect = M <= (uint32_t)kKeepCap;
     const Bound bn = bounded_select(n_next, M, nk, na, nn, compute_ranks, sm,
-                                    next_range, sm.nk_lo, sm.nk_hi);
+                                    next_range, sm.nk_lo, sm.nk_hi, collect);
+    // survivors already listed by the selection (keys above its boundary
+    // bin), and the boundary bin's size
+    const bool listed = !bn.all && sm.collected != 0;
+    const uint32_t n_listed = min(sm.n_keep, (uint32_t)kKeepCap);
+    const uint32_t n_bin = min(sm.n_out, (uint32_t)kBinCap);
+    __syncthreads();
     if (tid == 0) sm.n_out = 0;
     __syncthreads();
     const uint32_t keep_cnt = bn.all ? n_next : M;
@@ -1341,6 +1372,28 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       for (uint32_t i = tid; i < n_next; i += kBlock)
         if (i < a.lay.cur_cap && hist_used + i < hist_cap) emit(i, i);
       if (tid == 0) sm.n_out = n_next;
+    } else if (listed) {
+      // the boundary bin's survivors join the listed ones (a record is read
+      // only for a key on the boundary of a cut tie), then the records
+      if (tid == 0) sm.n_keep = n_listed;
+      __syncthreads();
+      for (uint32_t b = tid; b < n_bin + ((kBlock - n_bin % kBlock) % kBlock); b += kBlock) {
+        bool keep = false;
+        uint32_t i = 0;
+        if (b < n_bin) {
+          const uint64_t key = ~sm.bin_key[b];
+          i = sm.bin_idx[b];
+          keep = key > bn.vkey ||
+                 (key == bn.vkey && (!bn.tie || bound_keep(bn, key, na(i), nn(i))));
+        }
+        const uint32_t q = wave_append(keep, &sm.n_keep);
+        if (keep && q < (uint32_t)kKeepCap) sm.keep_idx[q] = i;
+      }
+      __syncthreads();
+      const uint32_t nk2 = min(sm.n_keep, (uint32_t)kKeepCap);
+      for (uint32_t o = tid; o < nk2; o += kBlock)
+        if (o < a.lay.cur_cap && hist_used + o < hist_cap) emit(sm.keep_idx[o], o);
+      if (tid == 0) sm.n_out = sm.n_keep;
     } else if (keep_cnt <= (uint32_t)kKeepCap) {
       // positions of the survivors first (from the keys alone; the rest of
       // a record is read only for a key on the boundary of a cut tie), then
