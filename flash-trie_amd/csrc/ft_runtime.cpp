@@ -478,7 +478,8 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
                                  8ull * kStepStats * max_steps + 8, 256);
   // per request: lnf + beams + ids + logps + row flags + permutation
   c->per_req = align_up(8 * (max_steps + 1), 16) + align_up(4 * max_steps, 16) +
-               3 * align_up(4 * max_steps * K, 16) + align_up(max_steps, 16) + 256;
+               3 * align_up(4 * max_steps * K, 16) + align_up(max_steps, 16) +
+               align_up(16 * max_steps, 16) + 256;
   hipError_t e;
   if ((e = hipMalloc(&c->d_ws, c->ws_stride * max_batch)) != hipSuccess)
     return release_workspace(c), hip_fail(e, "hipMalloc(workspace)");
@@ -494,6 +495,15 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   c->staged.clear();
   c->launched = false;
   return FT_OK;
+}
+
+// The order-preserving 64-bit key of a double that the device computes for
+// every norm (-0.0 and +0.0 map alike).
+static uint64_t host_norm_key(double v) {
+  if (v == 0.0) v = 0.0;
+  uint64_t b;
+  std::memcpy(&b, &v, 8);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
 int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
@@ -596,6 +606,36 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
       }
       rowflag[t] = sorted ? 0 : 1;
       any_perm |= !sorted;
+    }
+    // Per step, bounds of the keys pushed into `next`: a push's score is a
+    // parent score plus a logp that passes the token threshold, and itself
+    // passes the sentence threshold; parent scores are bounded by the same
+    // recursion one step earlier.  Double additions and the multiplication
+    // by the length factor are monotone, so the bounds hold exactly for the
+    // device's arithmetic (which this repeats).
+    d.kb_off = (uint32_t)o;
+    uint64_t* kb = (uint64_t*)(base + o);
+    o = align_up(o + 16ull * T, 16);
+    {
+      double s_lo = 0.0, s_hi = 0.0;  // parent scores at step t
+      for (uint32_t t = 0; t < T; ++t) {
+        const float* rlp = lps + (uint64_t)t * K;
+        double x_lo = 0.0, x_hi = 0.0;
+        bool any = false;
+        for (uint32_t k = 0; k < K; ++k) {
+          const double x = (double)rlp[k];
+          if (x <= (double)q.token_logp_threshold) continue;  // never pushed
+          if (!any || x < x_lo) x_lo = x;
+          if (!any || x > x_hi) x_hi = x;
+          any = true;
+        }
+        const double lo = std::max(q.sent_logp_threshold, s_lo + x_lo);
+        const double hi = s_hi + x_hi;
+        kb[2 * t] = host_norm_key(lo * lnf[t + 1]);
+        kb[2 * t + 1] = host_norm_key(hi * lnf[t + 1]);
+        s_lo = lo;
+        s_hi = hi;
+      }
     }
     d.perm_off = 0;
     if (any_perm) {

@@ -27,7 +27,7 @@ enum : uint32_t {
 struct DevReq {
   uint32_t T, K, F, flags;
   float tok_thr;
-  uint32_t pad0;
+  uint32_t kb_off;     // u64[2T]: per step, bounds of its next-list keys
   double sent_thr;
   uint64_t in_off;     // byte offset of this request's block in the stage
   uint32_t beams_off;  // lnf[T + 1] (f64) sits at offset 0

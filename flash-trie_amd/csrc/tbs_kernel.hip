@@ -88,8 +88,7 @@ struct Smem {
   // selection
   uint32_t hist[256];
   uint64_t red64[2 * kWaves];
-  double redd[4][kWaves];
-  unsigned long long nk_lo, nk_hi;  // bounds of the step's next-list keys
+
   uint32_t wsum[kWaves];
   uint32_t sel_digit, sel_cum, sel_cnt;
   uint32_t n_keep, collected;
@@ -330,9 +329,13 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     *rem_out = need;
     return mn;
   }
-  // bits above `top` are common to every candidate
-  int top = 63 - __clzll((long long)(mn ^ mx));
-  uint64_t prefix = mn & ~((top >= 63) ? ~0ull : ((2ull << top) - 1ull));
+  // Digits are taken from the offset k - mn (order-preserving for k >= mn):
+  // a range that straddles a power of two in the raw key (an exponent
+  // boundary of the doubles behind the keys) would otherwise put most keys
+  // in a few bins of the first window.  Offsets above bit `top` are zero.
+  const uint64_t base = mn;
+  int top = 63 - __clzll((long long)(mx - mn));
+  uint64_t prefix = 0;
   uint32_t rem = need;
   uint32_t cnt = n;
   for (;;) {
@@ -343,8 +346,9 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     for (uint32_t i = tid; i < nb; i += kBlock) sm.whist[i] = 0;
     __syncthreads();
     visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
-      const bool act = ok && (k & hi_mask) == prefix;
-      hist_add(act, (uint32_t)((k >> sh) & (nb - 1)), sm.whist);
+      const uint64_t o = k - base;
+      const bool act = ok && (o & hi_mask) == prefix;
+      hist_add(act, (uint32_t)((o >> sh) & (nb - 1)), sm.whist);
     });
     __syncthreads();
     // the bin holding the rem-th key: each thread owns nb / kBlock bins
@@ -380,7 +384,7 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     if (sh == 0) {
       *eq = cnt;
       *rem_out = rem;
-      return prefix;
+      return prefix + base;
     }
     top = sh - 1;
     if (cnt <= (uint32_t)kBinCap) break;
@@ -395,7 +399,7 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     }
     __syncthreads();
     visit_keys(n, gk, [&](uint32_t i, bool ok, uint64_t k) {
-      const uint64_t hk = k & hi_mask;
+      const uint64_t hk = (k - base) & hi_mask;
       const bool act = ok && hk == prefix;
       const uint32_t o = wave_append(act, &sm.n_out);
       if (act && o < (uint32_t)kBinCap) {
@@ -419,9 +423,9 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     for (uint32_t i = tid; i < 256; i += kBlock) sm.hist[i] = 0;
     __syncthreads();
     for (uint32_t i = tid; i < cnt; i += kBlock) {
-      const uint64_t k = sm.bin_key[i];
-      const bool act = (k & msk) == prefix;
-      hist_add(act, (uint32_t)((k >> s0) & (nb - 1)), sm.hist);
+      const uint64_t o = sm.bin_key[i] - base;
+      const bool act = (o & msk) == prefix;
+      hist_add(act, (uint32_t)((o >> s0) & (nb - 1)), sm.hist);
     }
     __syncthreads();
     hist_pick(rem, sm);
@@ -432,7 +436,7 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
     if (s0 == 0) {
       *eq = c2;
       *rem_out = rem;
-      return prefix;
+      return prefix + base;
     }
     top = s0 - 1;
     if (c2 == 1) {
@@ -440,7 +444,7 @@ __device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
       const uint64_t m2 = ~((2ull << top) - 1ull);
       for (uint32_t i = tid; i < cnt; i += kBlock) {
         const uint64_t k = sm.bin_key[i];
-        if ((k & m2) == prefix) sm.red64[0] = k;
+        if (((k - base) & m2) == prefix) sm.red64[0] = k;
       }
       __syncthreads();
       const uint64_t r = sm.red64[0];
@@ -1175,50 +1179,10 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       row[7] = w_pr;
     }
 
-    // ---- bounds of the next-list keys, from LDS ----------------------------
-    // A push's score is a parent score plus a proposal logp and its key a
-    // monotone function of the score (rounding is monotone too), so the
-    // extreme parent scores and logps bound every key: the selection needs
-    // no pass over the list for its range.
+    // bounds of every key pushed into `next` at this step, from the staged
+    // request (the selection then needs no pass over the list for its range)
     const uint32_t Mnext = beams[t];
-    const bool next_range = n_next > Mnext && n_cur <= (uint32_t)kBlock;
-    if (next_range) {
-      double smin = __builtin_huge_val(), smax = -__builtin_huge_val();
-      double xmin = __builtin_huge_val(), xmax = -__builtin_huge_val();
-      for (uint32_t j = tid; j < n_cur; j += kBlock) {
-        smin = min(smin, sm.p_s[j]);
-        smax = max(smax, sm.p_s[j]);
-      }
-      for (uint32_t p = tid; p < K; p += kBlock) {
-        xmin = min(xmin, (double)sm.row_lp[p]);
-        xmax = max(xmax, (double)sm.row_lp[p]);
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        smin = min(smin, __shfl_xor(smin, o, 64));
-        smax = max(smax, __shfl_xor(smax, o, 64));
-        xmin = min(xmin, __shfl_xor(xmin, o, 64));
-        xmax = max(xmax, __shfl_xor(xmax, o, 64));
-      }
-      if ((tid & 63u) == 0) {
-        sm.redd[0][tid >> 6] = smin;
-        sm.redd[1][tid >> 6] = smax;
-        sm.redd[2][tid >> 6] = xmin;
-        sm.redd[3][tid >> 6] = xmax;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        for (int w = 1; w < kWaves; ++w) {
-          smin = min(smin, sm.redd[0][w]);
-          smax = max(smax, sm.redd[1][w]);
-          xmin = min(xmin, sm.redd[2][w]);
-          xmax = max(xmax, sm.redd[3][w]);
-        }
-        sm.nk_lo = norm_key((smin + xmin) * lnf_next);
-        sm.nk_hi = norm_key((smax + xmax) * lnf_next);
-      }
-      __syncthreads();
-    }
+    const uint64_t* kbound = (const uint64_t*)(in + d.kb_off) + 2ull * t;
 
     // ---- parent ranks (only when arrival order is needed) ---------------
     bool ranks_done = false;
@@ -1340,8 +1304,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
     const bool collect = M <= (uint32_t)kKeepCap;
+    const uint64_t nk_lo = kbound[0], nk_hi = kbound[1];
     const Bound bn = bounded_select(n_next, M, nk, na, nn, compute_ranks, sm,
-                                    next_range, sm.nk_lo, sm.nk_hi, collect);
+                                    nk_lo <= nk_hi, nk_lo, nk_hi, collect);
     // survivors already listed by the selection (keys above its boundary
     // bin), and the boundary bin's size
     const bool listed = !bn.all && sm.collected != 0;
