@@ -130,6 +130,7 @@ def beam_sweep(ft, trie, vocab, T, widths, steps, warmup, rules, ot=None):
                                     True, 0, model=1)
         beams = np.full((P, T), B, dtype=np.uint32)
         ft.stage(trie, beams, ids, lp, tok_thr, sent_thr, ALPHA, early)
+        ft.launch(trie, 0, 3)  # untimed separator launch for kernel traces
         for i in range(warmup):
             ft.launch(trie, i % P, 1)
         ft.sync(trie)
@@ -244,6 +245,8 @@ def main():
     # ---- batch-1 latency through the C++ boundary (host arrays) -----------
     bl = []
     nbd = min(args.boundary, P)
+    ft.launch(trie, 0, min(3, P))  # untimed separator launch for kernel traces
+    ft.sync(trie)
     for r in range(nbd):
         t0 = time.perf_counter()
         ft.stage(trie, beams[r:r + 1], ids[r:r + 1], lp[r:r + 1], TOK_THR,
