@@ -88,7 +88,6 @@ struct ft_ctx {
                               // a lone request gets every CU)
   uint32_t share_min = 8192;  // work items from which a step is shared
   int max_resident = 0;
-  uint32_t epoch = 0;
   // ring of (start, end) event pairs, one pair per launch
   static constexpr size_t kRing = 1024;
   std::vector<hipEvent_t> ring;
@@ -428,6 +427,12 @@ int ft_create(const void* image, size_t image_bytes, int device,
   return FT_OK;
 }
 
+// Launch epochs tag the control words a request's workgroups sync through.
+// They come from one process-wide counter, so no launch of any context ever
+// reuses one: a workspace may sit on memory another context freed, and a
+// stale control word must never look like a step posted by this launch.
+static std::atomic<uint32_t> g_launch_epoch{0};
+
 int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
                size_t max_out_beams, size_t max_out_tokens,
                size_t max_inter_beams) {
@@ -465,9 +470,6 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   L.par_node = off; off = align_up(off + B * 4, 256);
   L.par_mode = off; off = align_up(off + B * 4, 256);
   L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
-  L.row_id = off; off = align_up(off + K * 4, 256);
-  L.row_lp = off; off = align_up(off + K * 4, 256);
-  L.row_k = off; off = align_up(off + K * 2, 256);
   L.next_cap = (uint32_t)BK;
   L.sel_cap = (uint32_t)(BK + B);
   L.hist_cap = (uint32_t)max_inter_beams;
@@ -476,13 +478,16 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   c->ws_stride = off;
   c->out_slot_max = align_up(step_stats_offset((uint32_t)B, 0) + 4 * (uint64_t)max_out_tokens +
                                  8ull * kStepStats * max_steps + 8, 256);
-  // per request: lnf + beams + ids + logps + row flags + permutation
+  // per request: lnf + beams + sorted rows (token, logp, index) + key bounds
   c->per_req = align_up(8 * (max_steps + 1), 16) + align_up(4 * max_steps, 16) +
-               3 * align_up(4 * max_steps * K, 16) + align_up(max_steps, 16) +
+               2 * align_up(4 * max_steps * K, 16) + align_up(2 * max_steps * K, 16) +
                align_up(16 * max_steps, 16) + 256;
   hipError_t e;
   if ((e = hipMalloc(&c->d_ws, c->ws_stride * max_batch)) != hipSuccess)
     return release_workspace(c), hip_fail(e, "hipMalloc(workspace)");
+  // control blocks start at "nothing posted" (epoch 0 is never used)
+  if ((e = hipMemset(c->d_ws, 0, c->ws_stride * max_batch)) != hipSuccess)
+    return release_workspace(c), hip_fail(e, "hipMemset(workspace)");
   int rc = alloc_staging(c, max_batch);
   if (rc) return release_workspace(c), rc;
   c->max_batch = max_batch;
@@ -581,22 +586,21 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     d.beams_off = (uint32_t)o;
     std::memcpy(base + o, q.beams, 4ull * T);
     o = align_up(o + 4ull * T, 16);
-    d.ids_off = (uint32_t)o;
-    uint32_t* ids = (uint32_t*)(base + o);
+    d.rid_off = (uint32_t)o;
+    uint32_t* rid_s = (uint32_t*)(base + o);
     o = align_up(o + 4ull * T * K, 16);
-    d.lp_off = (uint32_t)o;
-    float* lps = (float*)(base + o);
+    d.rlp_off = (uint32_t)o;
+    float* rlp_s = (float*)(base + o);
     o = align_up(o + 4ull * T * K, 16);
-    d.rowflag_off = (uint32_t)o;
-    uint8_t* rowflag = base + o;
-    o = align_up(o + T, 16);
-    bool any_perm = false;
+    d.rk_off = (uint32_t)o;
+    uint16_t* rk_s = (uint16_t*)(base + o);
+    o = align_up(o + 2ull * T * K, 16);
+    // rows in ascending token order, with each proposal's index in the
+    // caller's row (the order the reference visits proposals in)
     for (uint32_t t = 0; t < T; ++t) {
       const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
       const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
       if (!rid || !rlp) return fail(FT_E_ARG, who + "null topk row");
-      std::memcpy(ids + (uint64_t)t * K, rid, 4ull * K);
-      std::memcpy(lps + (uint64_t)t * K, rlp, 4ull * K);
       bool sorted = true;
       for (uint32_t k = 0; k < K; ++k) {
         const float x = rlp[k];
@@ -604,8 +608,27 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
           return fail(FT_E_INPUT, who + "topk_logp holds NaN or +inf");
         if (k && rid[k] <= rid[k - 1]) sorted = false;
       }
-      rowflag[t] = sorted ? 0 : 1;
-      any_perm |= !sorted;
+      uint32_t* oid = rid_s + (uint64_t)t * K;
+      float* olp = rlp_s + (uint64_t)t * K;
+      uint16_t* ok = rk_s + (uint64_t)t * K;
+      if (sorted) {
+        std::memcpy(oid, rid, 4ull * K);
+        std::memcpy(olp, rlp, 4ull * K);
+        for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
+        continue;
+      }
+      tmp.resize(K);
+      for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
+      std::sort(tmp.begin(), tmp.end());
+      for (uint32_t p = 0; p < K; ++p) {
+        if (p && tmp[p].first == tmp[p - 1].first)
+          return fail(FT_E_INPUT, who + "duplicate token id " +
+                                      std::to_string(tmp[p].first) +
+                                      " in topk row " + std::to_string(t));
+        oid[p] = tmp[p].first;
+        olp[p] = rlp[tmp[p].second];
+        ok[p] = (uint16_t)tmp[p].second;
+      }
     }
     // Per step, bounds of the keys pushed into `next`: a push's score is a
     // parent score plus a logp that passes the token threshold, and itself
@@ -619,7 +642,7 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     {
       double s_lo = 0.0, s_hi = 0.0;  // parent scores at step t
       for (uint32_t t = 0; t < T; ++t) {
-        const float* rlp = lps + (uint64_t)t * K;
+        const float* rlp = rlp_s + (uint64_t)t * K;
         double x_lo = 0.0, x_hi = 0.0;
         bool any = false;
         for (uint32_t k = 0; k < K; ++k) {
@@ -635,26 +658,6 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
         kb[2 * t + 1] = host_norm_key(hi * lnf[t + 1]);
         s_lo = lo;
         s_hi = hi;
-      }
-    }
-    d.perm_off = 0;
-    if (any_perm) {
-      d.perm_off = (uint32_t)o;
-      uint32_t* perm = (uint32_t*)(base + o);
-      o = align_up(o + 4ull * T * K, 16);
-      for (uint32_t t = 0; t < T; ++t) {
-        if (!rowflag[t]) continue;
-        const uint32_t* rid = ids + (uint64_t)t * K;
-        tmp.resize(K);
-        for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
-        std::sort(tmp.begin(), tmp.end());
-        for (uint32_t k = 0; k < K; ++k) {
-          if (k && tmp[k].first == tmp[k - 1].first)
-            return fail(FT_E_INPUT, who + "duplicate token id " +
-                                        std::to_string(tmp[k].first) +
-                                        " in topk row " + std::to_string(t));
-          perm[(uint64_t)t * K + k] = tmp[k].second;
-        }
       }
     }
     off = align_up(off + o, 256);
@@ -705,7 +708,9 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   const uint32_t fit = (uint32_t)std::max<int>(1, c->max_resident / (int)count);
   a.wgs = std::max(1u, std::min(c->wgs_req, fit));
   a.share_min = c->share_min;
-  a.epoch = ++c->epoch;
+  uint32_t ep = ++g_launch_epoch;
+  if (ep == 0) ep = ++g_launch_epoch;
+  a.epoch = ep;
   a.wdir = c->d_wdir;
   a.wtab = c->d_wtab;
   a.labels = c->d_labels;

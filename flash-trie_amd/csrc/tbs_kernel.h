@@ -31,10 +31,12 @@ struct DevReq {
   double sent_thr;
   uint64_t in_off;     // byte offset of this request's block in the stage
   uint32_t beams_off;  // lnf[T + 1] (f64) sits at offset 0
-  uint32_t ids_off;
-  uint32_t lp_off;
-  uint32_t rowflag_off;  // uint8_t[T]: 1 if row t is permuted
-  uint32_t perm_off;     // uint32_t[T * K] or 0
+  // proposal rows in ascending token order: token (u32[T * K]), logp
+  // (f32[T * K]) and the proposal's index in the caller's row (u16[T * K])
+  uint32_t rid_off;
+  uint32_t rlp_off;
+  uint32_t rk_off;
+  uint32_t pad0;
   uint32_t out_T;        // token stride of the output rows
 };
 
@@ -47,7 +49,7 @@ struct CurRec {     // a hypothesis kept in the beam
 struct NextRec {    // a push into `next`
   uint64_t key;     // order-preserving norm
   uint32_t node;
-  uint32_t jk;      // parent slot << 16 | proposal index
+  uint32_t jk;      // parent slot << 16 | position in the token-sorted row
 };
 
 struct SelRec {     // a push into `selected`
@@ -146,7 +148,6 @@ static_assert(sizeof(Ctl) == 384, "Ctl layout");
 struct WsLayout {   // byte offsets inside one request's workspace slot
   uint64_t cur0, cur1, nextc, selA, selB, rank, hist;
   uint64_t ctl, par_c0, par_aux, par_node, par_mode, par_woff;
-  uint64_t row_id, row_lp, row_k;
   uint32_t next_cap, sel_cap, hist_cap, cur_cap;
 };
 

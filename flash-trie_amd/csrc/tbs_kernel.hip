@@ -96,6 +96,7 @@ struct Smem {
   uint32_t status;
   unsigned long long cnt_parents, cnt_children, cnt_probes;
   unsigned long long bcast;
+  uint32_t hstep[6];  // a helper's view of the posted step
   uint32_t w_children, w_probes;
 };
 // rank scratch aliases the row arrays (used after expansion only)
@@ -561,23 +562,11 @@ __device__ __forceinline__ unsigned long long ld_relaxed(const unsigned long lon
 __device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint16_t ld_relaxed_u16(const uint16_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_relaxed_f(const float* p) {
-  return __uint_as_float(ld_relaxed((const uint32_t*)p));
-}
 __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_u16(uint16_t* p, uint16_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev_f(float* p, float v) {
-  st_dev((uint32_t*)p, __float_as_uint(v));
 }
 __device__ __forceinline__ unsigned long long pack2(uint32_t lo, uint32_t hi) {
   return (unsigned long long)lo | ((unsigned long long)hi << 32);
@@ -726,7 +715,7 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
       }
       if (pos >= 0) {
         const float x = sm.row_lp[pos];
-        k = sm.row_k[pos];
+        k = (uint32_t)pos;
         tok = sm.row_id[pos];
         const double ps = lds_par ? sm.p_s[pj] : ld_cur(&v.cur[pj]).s;
         // thresholds in double, `<=` drops (louds-trie.cc:87-90)
@@ -862,17 +851,15 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
   }
 }
 
-// Loads the proposal row of step t into LDS in ascending token order.
-__device__ void load_row(const uint32_t* ids, const float* lps,
-                         const uint32_t* perm, bool permuted, uint32_t t,
-                         uint32_t K, Smem& sm) {
-  const uint32_t* rid = ids + (uint64_t)t * K;
-  const float* rlp = lps + (uint64_t)t * K;
+// Loads the proposal row of step t (staged in ascending token order) into
+// LDS.
+__device__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
+                         uint32_t t, uint32_t K, Smem& sm) {
+  const uint64_t o = (uint64_t)t * K;
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
-    const uint32_t k = permuted ? perm[(uint64_t)t * K + p] : p;
-    sm.row_id[p] = rid[k];
-    sm.row_lp[p] = rlp[k];
-    sm.row_k[p] = (uint16_t)k;
+    sm.row_id[p] = rid[o + p];
+    sm.row_lp[p] = rlp[o + p];
+    sm.row_k[p] = rk[o + p];
   }
 }
 
@@ -886,8 +873,9 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
   unsigned long long seen = tag;  // generation 0: nothing posted yet
   const uint8_t* in = a.stage + d.in_off;
   const double* lnf = (const double*)in;
-  const uint32_t* ids = (const uint32_t*)(in + d.ids_off);
-  const float* lps = (const float*)(in + d.lp_off);
+  const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
+  const float* rlp = (const float*)(in + d.rlp_off);
+  const uint16_t* rk = (const uint16_t*)(in + d.rk_off);
   for (;;) {
     if (tid == 0) {
       unsigned long long v = 0;
@@ -897,16 +885,27 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
         __builtin_amdgcn_s_sleep(1);
       }
       sm.bcast = v;
+      if ((v >> 32) == a.epoch && (uint32_t)v != kGoExit && v != seen) {
+        // the step's parameters, read once after `go` and shared through LDS
+        // so that every thread takes the same branches below
+        sm.hstep[0] = ld_relaxed(&ctl->t);
+        sm.hstep[1] = ld_relaxed(&ctl->W);
+        sm.hstep[2] = ld_relaxed(&ctl->n_par);
+        sm.hstep[3] = ld_relaxed(&ctl->nS);
+        sm.hstep[4] = ld_relaxed(&ctl->cur_which);
+        sm.hstep[5] = ld_relaxed(&ctl->sel_which);
+      }
     }
     __syncthreads();
     const unsigned long long v = sm.bcast;
+    const uint32_t t = sm.hstep[0], W = sm.hstep[1], n_par = sm.hstep[2],
+                   nS = sm.hstep[3], cur_which = sm.hstep[4], sel_which = sm.hstep[5];
     __syncthreads();
     if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
     seen = v;
-    const uint32_t t = ld_relaxed(&ctl->t), W = ld_relaxed(&ctl->W);
     StepView sv;
-    sv.cur = (const CurRec*)(ws + (ld_relaxed(&ctl->cur_which) ? a.lay.cur1 : a.lay.cur0));
-    sv.sel = (SelRec*)(ws + (ld_relaxed(&ctl->sel_which) ? a.lay.selB : a.lay.selA));
+    sv.cur = (const CurRec*)(ws + (cur_which ? a.lay.cur1 : a.lay.cur0));
+    sv.sel = (SelRec*)(ws + (sel_which ? a.lay.selB : a.lay.selA));
     sv.nextc = (NextRec*)(ws + a.lay.nextc);
     sv.pc0 = (const uint32_t*)(ws + a.lay.par_c0);
     sv.paux = (const uint32_t*)(ws + a.lay.par_aux);
@@ -914,26 +913,22 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
     sv.pmode = (const uint32_t*)(ws + a.lay.par_mode);
     sv.woff = (const uint32_t*)(ws + a.lay.par_woff);
     sv.ctl = ctl;
-    sv.n_par = ld_relaxed(&ctl->n_par);
+    sv.n_par = n_par;
     sv.K = d.K;
     sv.t = t;
-    sv.nS = ld_relaxed(&ctl->nS);
+    sv.nS = nS;
     sv.next_cap = a.lay.next_cap;
     sv.sel_cap = a.lay.sel_cap;
+    // a posted step always satisfies these bounds; anything else is not a
+    // step of this launch and is not expanded
+    const uint64_t max_w = (uint64_t)sv.n_par * max(a.scan_limit, d.K);
+    if (t >= d.T || sv.n_par == 0 || sv.n_par > a.lay.cur_cap ||
+        sv.nS > a.lay.sel_cap || (uint64_t)W > max_w)
+      continue;
     sv.lnf_next = lnf[t + 1];
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
-    // the sorted row, as the leader published it
-    const uint32_t* gid = (const uint32_t*)(ws + a.lay.row_id);
-    const float* glp = (const float*)(ws + a.lay.row_lp);
-    const uint16_t* gk = (const uint16_t*)(ws + a.lay.row_k);
-    for (uint32_t p = tid; p < d.K; p += kBlock) {
-      sm.row_id[p] = ld_relaxed(&gid[p]);
-      sm.row_lp[p] = ld_relaxed_f(&glp[p]);
-      sm.row_k[p] = ld_relaxed_u16(&gk[p]);
-    }
-    (void)ids;
-    (void)lps;
+    load_row(rid, rlp, rk, t, d.K, sm);
     __syncthreads();
     expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, false, sm);
     wait_stores();  // this slice's pushes and counters are complete
@@ -971,10 +966,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   const uint8_t* in = a.stage + d.in_off;
   const double* lnf = (const double*)in;
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
-  const uint32_t* ids = (const uint32_t*)(in + d.ids_off);
-  const float* lps = (const float*)(in + d.lp_off);
-  const uint32_t* perm = d.perm_off ? (const uint32_t*)(in + d.perm_off) : nullptr;
-  const uint8_t* rowflag = in + d.rowflag_off;
+  const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
+  const float* rlp = (const float*)(in + d.rlp_off);
+  const uint16_t* rk = (const uint16_t*)(in + d.rk_off);
   const uint32_t T = d.T, K = d.K, F = d.F;
   const bool early = (d.flags & kReqEarlyExit) != 0;
 
@@ -1014,7 +1008,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     if (n_cur == 0 || (early && nS >= F)) break;
     const unsigned long long t0 = wall_clock64();
     const uint32_t ncur0 = n_cur;
-    load_row(ids, lps, perm, perm && rowflag[t] != 0, t, K, sm);
+    load_row(rid, rlp, rk, t, K, sm);
     const double lnf_next = lnf[t + 1];
 
     // ---- parents: lookup mode, work items, exclusive prefix ---------------
@@ -1112,15 +1106,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
 
     const bool shared = a.wgs > 1 && W >= a.share_min;
     if (shared) {
-      // publish the row and the step, then wake the helpers
-      uint32_t* gid = (uint32_t*)(ws + a.lay.row_id);
-      float* glp = (float*)(ws + a.lay.row_lp);
-      uint16_t* gk = (uint16_t*)(ws + a.lay.row_k);
-      for (uint32_t p = tid; p < K; p += kBlock) {
-        st_dev(&gid[p], sm.row_id[p]);
-        st_dev_f(&glp[p], sm.row_lp[p]);
-        st_dev_u16(&gk[p], sm.row_k[p]);
-      }
+      // publish the step (the helpers read the row from the staged request),
+      // then wake the helpers
       if (tid == 0) {
         st_dev(&ctl->n_next, 0u);
         st_dev(&ctl->n_sel, 0u);
@@ -1236,7 +1223,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       auto sel_arr = [&](uint32_t i) {
         const SelRec& r = selA[i];
         if (!r.isnew) return 0u;
-        return 1u + rank[r.jk >> 16] * K + (r.jk & 0xFFFFu);
+        return 1u + rank[r.jk >> 16] * K + sm.row_k[r.jk & 0xFFFFu];
       };
       auto sel_node = [&](uint32_t i) { return selA[i].node; };
       Bound b{0, 0, 0, 0, 1};
@@ -1300,7 +1287,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     auto nk = [&](uint32_t i) { return nextc[i].key; };
     auto na = [&](uint32_t i) {
       const uint32_t jk = nextc[i].jk;
-      return rank[jk >> 16] * K + (jk & 0xFFFFu);
+      return rank[jk >> 16] * K + sm.row_k[jk & 0xFFFFu];
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
     const bool collect = M <= (uint32_t)kKeepCap;
@@ -1324,12 +1311,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // survivor i becomes hypothesis o of the next beam
     auto emit = [&](uint32_t i, uint32_t o) {
       const NextRec c = nextc[i];
-      const uint32_t j = c.jk >> 16, k = c.jk & 0xFFFFu;
+      const uint32_t j = c.jk >> 16, q = c.jk & 0xFFFFu;
       const CurRec p = cur[j];
-      st_cur(&cur2[o], p.s + (double)lps[(uint64_t)t * K + k], c.node, hist_used + o);
+      st_cur(&cur2[o], p.s + (double)rlp[(uint64_t)t * K + q], c.node, hist_used + o);
       HistRec h;
       h.phist = p.hist;
-      h.tok = ids[(uint64_t)t * K + k];
+      h.tok = rid[(uint64_t)t * K + q];
       hist[hist_used + o] = h;
     };
     if (bn.all) {

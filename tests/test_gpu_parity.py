@@ -293,6 +293,34 @@ def test_shared_steps(ft, po, monkeypatch, wgs, share_min):
                                     f"wgs {wgs} req {b0 + i} {alpha} {early}")
 
 
+def test_fresh_contexts_shared_steps(ft, po, monkeypatch):
+    # contexts created and destroyed one after another, every step shared: a
+    # new workspace may sit on memory an earlier context used, so its control
+    # words start cleared and launch epochs never repeat across contexts --
+    # helpers act only on steps their own leader posts
+    monkeypatch.setenv("FT_WGS", "16")
+    monkeypatch.setenv("FT_SHARE_MIN", "0")
+    toks, offs = ft.synth_keys(30000, 4096, 3, 8, 1.1, 9)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    shapes = [(4, 32, 16), (2, 64, 32), (4, 32, 16), (1, 16, 8), (3, 48, 24)]
+    for rnd, (batch, topk, beams) in enumerate(shapes):
+        print("fresh context", rnd, batch, topk, beams, flush=True)
+        t = _gpu_trie(ft, toks=toks, offs=offs, batch=batch, topk=topk,
+                      steps=8, beams=beams, inter=4096)
+        ids, lp = ft.synth_requests(t, rnd, batch, 4096, 8, topk, beams, 0.3,
+                                    2.0, True, 3, model=1)
+        for early in (False, True):
+            got = ft.bs_tbs_gpu(t, batch, [[beams] * 8] * batch,
+                                [ids[i].tolist() for i in range(batch)],
+                                [lp[i].tolist() for i in range(batch)],
+                                -10.0, -40.0, 5.0, early)
+            for i in range(batch):
+                want = o.tbs([beams] * 8, ids[i], lp[i], -10.0, -40.0, 5.0, early)
+                assert_same_results((got[0][i], got[1][i]), want,
+                                    f"context {rnd} req {i} early {early}")
+        del t
+
+
 @pytest.mark.parametrize("alpha,early", [(0.0, False), (0.0, True), (5.0, False)])
 def test_wide_tied_selection(ft, po, alpha, early):
     # 4096 proposals into a 6000-way root with three logp values: thousands
