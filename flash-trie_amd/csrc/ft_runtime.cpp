@@ -83,7 +83,10 @@ struct ft_ctx {
   std::vector<StagedReq> staged;
   uint64_t out_stride = 0;
   bool launched = false;
-  uint32_t scan_mult = 8;
+  // parents with at most scan_mult * K children are scanned (one work item
+  // per child), wider ones use their hash table (K items): scanning a child
+  // is a coalesced 4-B read, a hashed proposal a random 64-B bucket
+  uint32_t scan_mult = 2;
   uint32_t wgs_req = 4096;    // workgroups per request (clamped to residency:
                               // a lone request gets every CU)
   uint32_t share_min = 8192;  // work items from which a step is shared

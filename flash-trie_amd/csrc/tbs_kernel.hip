@@ -51,6 +51,15 @@ constexpr int kKeepCap = 4096;
 // expansion: pushes a workgroup buffers in LDS before one global append
 constexpr int kPushCap = 1024;
 constexpr int kPushSelCap = 256;
+// expansion: an LDS hash of the row, token -> sorted position (linear
+// probing, load <= 1/2), built for rows of up to kRowHashMaxK proposals
+constexpr int kRowHashLog2 = 12;
+constexpr int kRowHash = 1 << kRowHashLog2;
+constexpr uint32_t kRowHashMaxK = kRowHash / 2;
+constexpr uint32_t kRowHashEmpty = 0xFFFFFFFFu;
+// the leader hashes the row for steps of at least this many work items (a
+// smaller step does too few lookups to repay the build)
+constexpr uint32_t kRowHashMinWork = 2048;
 
 struct Smem {
   // expansion: the current proposal row in ascending token order
@@ -69,6 +78,9 @@ struct Smem {
       uint32_t p_hist[kBlock];
       double p_s[kBlock];
       uint8_t p_mode[kBlock];
+      // the row hash (see kRowHash)
+      uint32_t rh_tok[kRowHash];
+      uint16_t rh_pos[kRowHash];
     };
     // selection: positions of the kept candidates, and the keys and
     // positions of one histogram bin
@@ -535,9 +547,25 @@ __device__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node_rec r,
   return 0xFFFFFFFFu;
 }
 
-// position of tok in the sorted LDS row, or -1
+__device__ __forceinline__ uint32_t row_hash(uint32_t tok) {
+  return (tok * 0x9E3779B1u) >> (32 - kRowHashLog2);
+}
+
+// position of tok in the sorted LDS row, or -1: a probe or two when the row
+// is hashed, else a binary search
 __device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
-                                        uint32_t tok) {
+                                        uint32_t tok, bool hashed) {
+  if (hashed) {
+    uint32_t h = row_hash(tok);
+    for (int it = 0; it < kRowHash; ++it) {
+      const uint32_t e = sm.rh_tok[h];
+      const uint32_t p = sm.rh_pos[h];
+      if (e == kRowHashEmpty) return -1;
+      if (e == tok) return (int)p;
+      h = (h + 1) & (kRowHash - 1);
+    }
+    return -1;
+  }
   uint32_t lo = 0, hi = K;
   while (lo < hi) {
     const uint32_t mid = (lo + hi) >> 1;
@@ -643,7 +671,7 @@ struct StepView {
 // sm.w_probes).
 __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
                              uint32_t gwave0, uint32_t nwaves, bool par_in_lds,
-                             bool solo, Smem& sm) {
+                             bool solo, bool hashed, Smem& sm) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const bool lds_par = v.n_par <= (uint32_t)kBlock;
   if (lds_par && !par_in_lds) {
@@ -700,14 +728,14 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
       ft_node_rec cr;
       bool have_child = false, label_sel = false;
       if (md == M_LP_NEXT || md == M_LP_SEL) {
-        pos = row_find(sm, K, aux);
+        pos = row_find(sm, K, aux, hashed);
         cnode = lds_par ? sm.p_node[pj] : ld_relaxed(&v.pnode[pj]);
       } else if (md == M_SCAN) {
         // the child's label: its first token, and whether it closes a key
         cnode = c0 + q;
         const uint32_t lw = a.labels[cnode];
         ++my_children;
-        pos = row_find(sm, K, lw & kTokMask);
+        pos = row_find(sm, K, lw & kTokMask, hashed);
         have_child = true;
         label_sel = (lw & kSlotSel) && depth_ok;
       } else if (md == M_SEARCH || md == M_HASH) {
@@ -852,15 +880,38 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
 }
 
 // Loads the proposal row of step t (staged in ascending token order) into
-// LDS.
+// LDS, and empties the row hash when the row is small enough to be hashed.
 __device__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
                          uint32_t t, uint32_t K, Smem& sm) {
   const uint64_t o = (uint64_t)t * K;
+  if (K <= kRowHashMaxK)
+    for (uint32_t i = threadIdx.x; i < (uint32_t)kRowHash; i += kBlock)
+      sm.rh_tok[i] = kRowHashEmpty;
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
     sm.row_id[p] = rid[o + p];
     sm.row_lp[p] = rlp[o + p];
     sm.row_k[p] = rk[o + p];
   }
+}
+
+// Hashes the LDS row (K <= kRowHashMaxK; the workgroup has synchronised since
+// load_row).  Tokens >= 2^31 - 1 never match a trie token and are left out.
+// Row tokens are distinct (staging rejects duplicates) and fill at most half
+// the table, so every insert ends in a free slot.  Ends synchronised.
+__device__ void hash_row(uint32_t K, Smem& sm) {
+  for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
+    const uint32_t tok = sm.row_id[p];
+    if (tok >= kTokMask) continue;
+    uint32_t h = row_hash(tok);
+    for (int it = 0; it < kRowHash; ++it) {
+      if (atomicCAS(&sm.rh_tok[h], kRowHashEmpty, tok) == kRowHashEmpty) {
+        sm.rh_pos[h] = (uint16_t)p;
+        break;
+      }
+      h = (h + 1) & (kRowHash - 1);
+    }
+  }
+  __syncthreads();
 }
 
 // A helper workgroup: waits for shared steps of its request and expands its
@@ -930,7 +981,10 @@ __device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
     sv.sent_thr = d.sent_thr;
     load_row(rid, rlp, rk, t, d.K, sm);
     __syncthreads();
-    expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, false, sm);
+    const bool hashed = d.K <= kRowHashMaxK;
+    if (hashed) hash_row(d.K, sm);
+    expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, false,
+                 hashed, sm);
     wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
     if (tid == 0) atomicAdd(&ctl->done, 1u);
@@ -1125,7 +1179,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       __syncthreads();
       if (tid == 0) st_dev(&ctl->go, tag | ++gen);
     }
-    expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared, sm);
+    // (the parent table ended synchronised: the row and the emptied hash are
+    // visible)
+    const bool hashed = K <= kRowHashMaxK && W >= kRowHashMinWork;
+    if (hashed) hash_row(K, sm);
+    expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared,
+                 hashed, sm);
     if (shared) {
       if (tid == 0) {
         for (uint32_t it = 0; it < kSpinLimit; ++it) {

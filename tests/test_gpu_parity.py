@@ -243,10 +243,10 @@ def test_beam_1000(ft, po):
 
 
 @pytest.mark.parametrize("scan_mult,wide_min", [("0", "0"), ("0", "2"),
-                                                ("1000000", "512"), ("1", "64")])
+                                                ("999999", "512"), ("1", "64")])
 def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min):
     # scan_mult 0 sends every parent with children to the binary search
-    # (wide_min 0) or the hash tables (wide_min 2); 1000000 scans all
+    # (wide_min 0) or the hash tables (wide_min 2); 999999 scans all
     monkeypatch.setenv("FT_SCAN_MULT", scan_mult)
     monkeypatch.setenv("FT_WIDE_MIN", wide_min)
     toks, offs = ft.synth_keys(50000, 4096, 3, 8, 1.1, 4)
