@@ -70,6 +70,7 @@ def build(verbose=False):
     host_objs = {
         "marisa_trie.cc": os.path.join(OBJ, "marisa_trie.o"),
         "image_builder.cc": os.path.join(OBJ, "image_builder.o"),
+        "marisa_format.cc": os.path.join(OBJ, "marisa_format.o"),
         "synth.cc": os.path.join(OBJ, "synth.o"),
         "synth_trie.cc": os.path.join(OBJ, "synth_trie.o"),
     }

@@ -25,6 +25,7 @@
 
 #include "../../include/flashtrie_amd.h"
 #include "image_builder.h"
+#include "marisa_format.h"
 #include "marisa.h"
 #include "synth.h"
 #include "trie_impl.h"
@@ -135,8 +136,17 @@ PYBIND11_MODULE(flashtrie, m) {
 
   py::class_<Trie>(m, "Trie")
       .def(py::init<>())
-      .def("load", [](Trie& t, const std::string& p) { t.load(p.c_str()); })
-      .def("mmap", [](Trie& t, const std::string& p) { t.mmap(p.c_str()); })
+      // a MARISA trie.bin written by the reference, or an image from save()
+      .def("load",
+           [](Trie& t, const std::string& p) {
+             py::gil_scoped_release nogil;
+             t.load(p.c_str());
+           })
+      .def("mmap",
+           [](Trie& t, const std::string& p) {
+             py::gil_scoped_release nogil;
+             t.mmap(p.c_str());
+           })
       .def("build",
            [](Trie& t, const std::vector<std::vector<uint32_t>>& rows) {
              marisa::Keyset ks;
@@ -149,6 +159,11 @@ PYBIND11_MODULE(flashtrie, m) {
       .def("num_keys", &Trie::num_keys)
       .def("num_nodes", &Trie::num_nodes)
       .def("save", [](const Trie& t, const std::string& p) { t.save(p.c_str()); })
+      .def("save_marisa",
+           [](const Trie& t, const std::string& p) {
+             py::gil_scoped_release nogil;
+             t.save_marisa(p.c_str());
+           })
       .def("clear", &Trie::clear)
       .def("get_max_batch_size", &Trie::get_max_batch_size)
       .def("init_tbs_gpu", &Trie::init_tbs_gpu, py::arg("max_batch_size"),
@@ -191,6 +206,29 @@ PYBIND11_MODULE(flashtrie, m) {
              return py::array_t<uint8_t>({(py::ssize_t)img.size()}, {(py::ssize_t)1},
                                          img.data(), self);
            })
+      .def("marisa_bytes",
+           [](const Trie& t) {
+             // the MARISA trie file save_marisa writes
+             std::vector<uint8_t> out;
+             std::string err;
+             if (!ftamd::marisa_from_image(image_of(t), &out, &err))
+               throw marisa::Exception(MARISA_FORMAT_ERROR, "marisa_bytes: " + err);
+             return py::array_t<uint8_t>((py::ssize_t)out.size(), out.data());
+           })
+      .def("load_marisa_bytes",
+           [](Trie& t, py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a) {
+             // a MARISA trie file held in memory (lib/marisa/trie.cc:34-42)
+             ftamd::ImageBlob img;
+             std::string err;
+             bool ok;
+             {
+               py::gil_scoped_release nogil;
+               ok = ftamd::image_from_marisa(a.data(), (size_t)a.size(), &img, &err);
+             }
+             if (!ok) throw marisa::Exception(MARISA_FORMAT_ERROR, "load_marisa_bytes: " + err);
+             t.assign_image(img.data(), img.size());
+           },
+           py::arg("data"))
       .def("assign_image",
            [](Trie& t, py::array_t<uint8_t, py::array::c_style | py::array::forcecast> a) {
              t.assign_image(a.data(), (size_t)a.size());

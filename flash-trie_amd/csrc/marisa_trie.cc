@@ -10,11 +10,14 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <memory>
 #include <queue>
 #include <string>
+#include <vector>
 
 #include "../../include/flashtrie_amd.h"
 #include "image_builder.h"
+#include "marisa_format.h"
 #include "trie_impl.h"
 
 namespace marisa {
@@ -237,23 +240,21 @@ void Trie::load(const char* filename) {
   if (!f) throw Exception(MARISA_IO_ERROR, std::string("load: cannot open ") + filename);
   const std::streamsize n = f.tellg();
   f.seekg(0);
-  char magic[16] = {0};
-  f.read(magic, std::min<std::streamsize>(16, n));
-  if (std::memcmp(magic, "We love Marisa.", 15) == 0)
-    throw Exception(MARISA_FORMAT_ERROR,
-                    std::string("load: ") + filename +
-                        " is a MARISA trie file; this library reads trie images "
-                        "written by Trie.save");
-  f.seekg(0);
-  std::vector<char> buf((size_t)n);
-  if (n > 0 && !f.read(buf.data(), n))
+  std::vector<uint64_t> buf(((size_t)n + 7) / 8);  // 8-byte aligned
+  if (n > 0 && !f.read((char*)buf.data(), n))
     throw Exception(MARISA_IO_ERROR, std::string("load: read failed on ") + filename);
   auto fresh = std::unique_ptr<TrieImpl>(new TrieImpl());
-  if (!fresh->img.assign(buf.data(), buf.size()))
-    throw Exception(MARISA_MEMORY_ERROR, "load: out of memory");
   std::string err;
-  if (!ftamd::validate_image(fresh->img, &err))
-    throw Exception(MARISA_FORMAT_ERROR, std::string("load: ") + err);
+  if (ftamd::is_marisa_file(buf.data(), (size_t)n)) {
+    // a trie.bin written by the reference (lib/marisa/trie.cc:44-53)
+    if (!ftamd::image_from_marisa((const uint8_t*)buf.data(), (size_t)n, &fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, std::string("load: ") + filename + ": " + err);
+  } else {
+    if (!fresh->img.assign(buf.data(), (size_t)n))
+      throw Exception(MARISA_MEMORY_ERROR, "load: out of memory");
+    if (!ftamd::validate_image(fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, std::string("load: ") + err);
+  }
   impl_.swap(fresh);
 }
 
@@ -266,6 +267,19 @@ void Trie::save(const char* filename) const {
   if (!f) throw Exception(MARISA_IO_ERROR, std::string("save: cannot open ") + filename);
   f.write((const char*)impl_->img.data(), (std::streamsize)impl_->img.size());
   if (!f) throw Exception(MARISA_IO_ERROR, std::string("save: write failed on ") + filename);
+}
+
+void Trie::save_marisa(const char* filename) const {
+  require_trie(impl_.get());
+  if (!filename) throw Exception(MARISA_NULL_ERROR, "save_marisa: null filename");
+  std::vector<uint8_t> bytes;
+  std::string err;
+  if (!ftamd::marisa_from_image(impl_->img, &bytes, &err))
+    throw Exception(MARISA_FORMAT_ERROR, "save_marisa: " + err);
+  std::ofstream f(filename, std::ios::binary);
+  if (!f) throw Exception(MARISA_IO_ERROR, std::string("save_marisa: cannot open ") + filename);
+  f.write((const char*)bytes.data(), (std::streamsize)bytes.size());
+  if (!f) throw Exception(MARISA_IO_ERROR, std::string("save_marisa: write failed on ") + filename);
 }
 
 void Trie::init_tbs_gpu(size_t max_batch_size, size_t max_num_topk,

@@ -35,10 +35,15 @@ class Trie {
   void build(Keyset& keyset, int config_flags = 0);
   void build(const std::vector<std::vector<Label>>& keys);
 
-  // Trie images in this library's format (see flashtrie_amd.h).
+  // load / mmap read either a MARISA trie file written by the reference
+  // (trie.bin: num_tries = 1, label order; lib/marisa/trie.cc:21-76) or a
+  // trie image in this library's format (flashtrie_amd.h), which save
+  // writes.  save_marisa writes the MARISA trie file the reference builds
+  // for the same keys.
   void load(const char* filename);
   void mmap(const char* filename);
   void save(const char* filename) const;
+  void save_marisa(const char* filename) const;
 
   void init_tbs_gpu(size_t max_batch_size, size_t max_num_topk = 1024,
                     size_t max_num_outpos = 64, size_t max_num_out_beams = 8192,

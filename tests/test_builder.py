@@ -80,10 +80,11 @@ def test_save_load_roundtrip(ft, tmp_path):
     assert np.array_equal(t.image(), m.image())
 
 
-def test_load_rejects_marisa_file(ft, tmp_path):
+def test_load_rejects_truncated_marisa_file(ft, tmp_path):
+    # a MARISA header followed by too few bytes for its sections
     p = tmp_path / "trie.bin"
     p.write_bytes(b"We love Marisa." + b"\0" * 64)
-    with pytest.raises(RuntimeError, match="MARISA"):
+    with pytest.raises(RuntimeError, match="truncated"):
         ft.Trie().load(str(p))
 
 

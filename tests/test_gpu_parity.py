@@ -321,6 +321,29 @@ def test_fresh_contexts_shared_steps(ft, po, monkeypatch):
         del t
 
 
+def test_trie_loaded_from_marisa_file(ft, po, tmp_path):
+    # a MARISA trie.bin (num_tries 1, label order) loaded and searched on the
+    # GPU: same node ids, so the same results as the oracle on the keys
+    toks, offs = ft.synth_keys(60000, 300000, 2, 9, 1.1, 12)
+    src = ft.Trie()
+    src.build_arrays(toks, offs)
+    p = str(tmp_path / "trie.bin")
+    src.save_marisa(p)
+    t = ft.Trie()
+    t.load(p)
+    t.init_tbs_gpu(4, max_num_topk=64, max_num_outpos=9, max_num_out_beams=32,
+                   max_num_out_tokens=32 * 9, max_num_inter_beams=4096)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 8, 300000, 9, 64, 32, 0.3, 2.0, True, 6, model=1)
+    for b0 in (0, 4):
+        got = ft.bs_tbs_gpu(t, 4, [[32] * 9] * 4, [ids[b0 + i].tolist() for i in range(4)],
+                            [lp[b0 + i].tolist() for i in range(4)], -10.0, -40.0, 5.0,
+                            b0 == 4)
+        for i in range(4):
+            want = o.tbs([32] * 9, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, b0 == 4)
+            assert_same_results((got[0][i], got[1][i]), want, f"marisa file req {b0 + i}")
+
+
 @pytest.mark.parametrize("alpha,early", [(0.0, False), (0.0, True), (5.0, False)])
 def test_wide_tied_selection(ft, po, alpha, early):
     # 4096 proposals into a 6000-way root with three logp values: thousands
