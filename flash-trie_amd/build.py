@@ -36,6 +36,7 @@ CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-ffp-contract=off",
 LIB_AMD = os.path.join(HERE, "libflashtrie_amd.so")
 LIB_MARISA = os.path.join(HERE, "libmarisa_amd.so")
 COPY_CALIB = os.path.join(HERE, "ft_copy_calib")
+BEAM_CLI = os.path.join(HERE, "ft-beam-search")
 
 
 def ext_suffix():
@@ -71,6 +72,7 @@ def build(verbose=False):
         "marisa_trie.cc": os.path.join(OBJ, "marisa_trie.o"),
         "image_builder.cc": os.path.join(OBJ, "image_builder.o"),
         "marisa_format.cc": os.path.join(OBJ, "marisa_format.o"),
+        "topk_io.cc": os.path.join(OBJ, "topk_io.o"),
         "synth.cc": os.path.join(OBJ, "synth.o"),
         "synth_trie.cc": os.path.join(OBJ, "synth_trie.o"),
     }
@@ -99,10 +101,14 @@ def build(verbose=False):
     _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", LIB_MARISA]
          + list(host_objs.values()) +
          ["-L" + HERE, "-lflashtrie_amd", "-Wl,-rpath,$ORIGIN"])
+    # the beam-search command line tool (tools/marisa-beam-search.cc)
+    _run([CXX] + CXX_FLAGS + [os.path.join(CSRC, "ft_beam_search.cc"), "-o", BEAM_CLI,
+                              "-L" + HERE, "-lmarisa_amd", "-lflashtrie_amd",
+                              "-Wl,-rpath,$ORIGIN"])
     _run([CXX, "-shared", "-fPIC", "-fopenmp", "-o", PYMOD, bind_obj,
           "-L" + HERE, "-lmarisa_amd", "-lflashtrie_amd",
           "-Wl,-rpath,$ORIGIN"])
-    return [LIB_AMD, LIB_MARISA, PYMOD, COPY_CALIB]
+    return [LIB_AMD, LIB_MARISA, PYMOD, COPY_CALIB, BEAM_CLI]
 
 
 def built():
