@@ -61,7 +61,7 @@ constexpr uint32_t kRowHashEmpty = 0xFFFFFFFFu;
 // smaller step does too few lookups to repay the build)
 constexpr uint32_t kRowHashMinWork = 2048;
 
-struct Smem {
+struct alignas(16) Smem {
   // expansion: the current proposal row in ascending token order
   uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
@@ -113,6 +113,36 @@ struct Smem {
 };
 // rank scratch aliases the row arrays (used after expansion only)
 constexpr int kRankChunk = 1024;
+static_assert(offsetof(Smem, row_id) % 16 == 0 && offsetof(Smem, row_lp) % 16 == 0,
+              "rank scratch is read 16 bytes at a time");
+static_assert(kRankChunk == kBlock, "a thread's own rank entry sits in its own chunk");
+
+// How many of the m LDS entries (rk_key[q], rk_node[q]) order before (k, n)
+// by (key, node).  Every thread reads the same entries (broadcast reads),
+// 2 * P keys per iteration through P 16-byte loads so the reads overlap; a
+// node is read only for an equal key.
+template <int P>
+__device__ __forceinline__ uint32_t count_before(const uint64_t* rk_key,
+                                                 const uint32_t* rk_node, uint32_t m,
+                                                 uint64_t k, uint32_t n) {
+  uint32_t c = 0, q = 0;
+  for (; q + 2 * P <= m; q += 2 * P) {
+    ulonglong2 v[P];
+#pragma unroll
+    for (int u = 0; u < P; ++u) v[u] = *(const ulonglong2*)&rk_key[q + 2 * u];
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      c += (v[u].x < k) + (v[u].y < k);
+      if (v[u].x == k) c += rk_node[q + 2 * u] < n;
+      if (v[u].y == k) c += rk_node[q + 2 * u + 1] < n;
+    }
+  }
+  for (; q < m; ++q) {
+    const uint64_t kk = rk_key[q];
+    c += (kk < k) || (kk == k && rk_node[q] < n);
+  }
+  return c;
+}
 
 // lookup mode word of a parent: the mode, and whether the parent sits at
 // string depth t (only then can a child -- one token long, terminal --
@@ -155,7 +185,7 @@ __device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
 }
 
 // Exclusive block scan of v over all kBlock threads.
-__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, Smem& sm) {
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, Smem& sm) {
   const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
   uint32_t x = v;
 #pragma unroll
@@ -201,7 +231,7 @@ __device__ __forceinline__ void hist_add(bool act, uint32_t digit,
 
 // Picks the bin holding the `rem`-th smallest item (1-based) from
 // sm.hist[256]; writes sel_digit / sel_cum (items in lower bins) / sel_cnt.
-__device__ void hist_pick(uint32_t rem, Smem& sm) {
+__device__ __forceinline__ void hist_pick(uint32_t rem, Smem& sm) {
   if (threadIdx.x < 64) {
     const uint32_t lane = threadIdx.x;
     const uint32_t h0 = sm.hist[4 * lane], h1 = sm.hist[4 * lane + 1],
@@ -236,7 +266,7 @@ __device__ void hist_pick(uint32_t rem, Smem& sm) {
 // i < n with filt(i).  Returns it; *eq = items equal to it, *rem = how many
 // of those are needed to reach `need`.
 template <typename KeyT, typename GetKey, typename Filt>
-__device__ KeyT radix_kth(uint32_t n, uint32_t need, GetKey gk, Filt filt,
+__device__ __forceinline__ KeyT radix_kth(uint32_t n, uint32_t need, GetKey gk, Filt filt,
                           Smem& sm, uint32_t* eq, uint32_t* rem_out) {
   constexpr int kBits = (int)sizeof(KeyT) * 8;
   KeyT prefix = 0, mask = 0;
@@ -303,7 +333,7 @@ __device__ __forceinline__ void visit_keys(uint32_t n, GetKey gk, F f) {
 // positions in sm.bin_idx, and sm.collected says that it ran: then a bounded
 // selection needs no further pass over the list.
 template <typename GetKey>
-__device__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
+__device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk, Smem& sm,
                             uint32_t* eq, uint32_t* rem_out, bool have_range,
                             uint64_t rmin, uint64_t rmax, bool collect = false) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -493,7 +523,7 @@ __device__ __forceinline__ bool bound_keep(const Bound& b, uint64_t key,
 // With `have_range`, every key(i) lies in [kmin, kmax].  With `collect`,
 // see kth_u64 (the items with a key above the boundary bin are listed).
 template <typename GetKey, typename GetArr, typename GetNode, typename Ranks>
-__device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
+__device__ __forceinline__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
                                 GetArr arr, GetNode node, Ranks need_ranks,
                                 Smem& sm, bool have_range = false,
                                 uint64_t kmin = 0, uint64_t kmax = ~0ull,
@@ -529,7 +559,7 @@ __device__ Bound bounded_select(uint32_t n, uint32_t M, GetKey key,
 }
 
 // KB(n)[j] for a link parent: walk up until the edge that covers position j.
-__device__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node_rec r,
+__device__ __forceinline__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node_rec r,
                              uint32_t j, uint32_t* err) {
   for (int guard = 0; guard < 65536; ++guard) {
     const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
@@ -669,7 +699,7 @@ struct StepView {
 // step alone: its LDS counters are the list lengths and the control block is
 // not used (the counts stay in sm.lq_next, sm.lq_sel, sm.w_children and
 // sm.w_probes).
-__device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
+__device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
                              uint32_t gwave0, uint32_t nwaves, bool par_in_lds,
                              bool solo, bool hashed, Smem& sm) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -881,7 +911,7 @@ __device__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
 
 // Loads the proposal row of step t (staged in ascending token order) into
 // LDS, and empties the row hash when the row is small enough to be hashed.
-__device__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
+__device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
                          uint32_t t, uint32_t K, Smem& sm) {
   const uint64_t o = (uint64_t)t * K;
   if (K <= kRowHashMaxK)
@@ -898,7 +928,7 @@ __device__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* 
 // load_row).  Tokens >= 2^31 - 1 never match a trie token and are left out.
 // Row tokens are distinct (staging rejects duplicates) and fill at most half
 // the table, so every insert ends in a free slot.  Ends synchronised.
-__device__ void hash_row(uint32_t K, Smem& sm) {
+__device__ __forceinline__ void hash_row(uint32_t K, Smem& sm) {
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
     const uint32_t tok = sm.row_id[p];
     if (tok >= kTokMask) continue;
@@ -916,7 +946,7 @@ __device__ void hash_row(uint32_t K, Smem& sm) {
 
 // A helper workgroup: waits for shared steps of its request and expands its
 // slice of the work items, until the leader posts the exit generation.
-__device__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
+__device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
                             uint32_t g, Smem& sm) {
   const uint32_t tid = threadIdx.x;
   Ctl* ctl = (Ctl*)(ws + a.lay.ctl);
@@ -1250,20 +1280,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         }
         for (uint32_t ib = 0; ib < ncur_now; ib += kRankChunk) {
           const uint32_t i = ib + tid;
-          if (tid < (uint32_t)kRankChunk) {
-            if (i < ncur_now) {
-              rk_key[tid] = norm_key(cur[i].s * lnf_cur);
-              rk_node[tid] = cur[i].node;
-            }
+          if (tid < (uint32_t)kRankChunk && i < ncur_now) {
+            // in the thread's own chunk, entry i is its own
+            rk_key[tid] = ib == jb ? myk : norm_key(cur[i].s * lnf_cur);
+            rk_node[tid] = ib == jb ? myn : cur[i].node;
           }
           __syncthreads();
           const uint32_t m = min((uint32_t)kRankChunk, ncur_now - ib);
-          if (j < ncur_now) {
-            for (uint32_t q = 0; q < m; ++q) {
-              const uint64_t kk = rk_key[q];
-              cntless += (kk < myk) || (kk == myk && rk_node[q] < myn);
-            }
-          }
+          if (j < ncur_now) cntless += count_before<4>(rk_key, rk_node, m, myk, myn);
           __syncthreads();
         }
         if (j < ncur_now) rank[j] = cntless;
@@ -1475,18 +1499,18 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         const uint32_t i = ib + tid;
         __syncthreads();
         if (tid < (uint32_t)kRankChunk && i < nS) {
-          const SelRec o = selA[i];
-          rk_key[tid] = norm_key(o.s * lnf[o.depth]);
-          rk_node[tid] = o.node;
+          if (ib == jb) {  // entry i is the thread's own
+            rk_key[tid] = myk;
+            rk_node[tid] = myn;
+          } else {
+            const SelRec o = selA[i];
+            rk_key[tid] = norm_key(o.s * lnf[o.depth]);
+            rk_node[tid] = o.node;
+          }
         }
         __syncthreads();
         const uint32_t m = min((uint32_t)kRankChunk, nS - ib);
-        if (j < nS) {
-          for (uint32_t q = 0; q < m; ++q) {
-            const uint64_t kk = rk_key[q];
-            cntless += (kk < myk) || (kk == myk && rk_node[q] < myn);
-          }
-        }
+        if (j < nS) cntless += count_before<4>(rk_key, rk_node, m, myk, myn);
       }
       if (j < nS && cntless < F) {
         onorm[cntless] = me.s * lnf[me.depth];
