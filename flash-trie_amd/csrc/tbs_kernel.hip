@@ -109,6 +109,7 @@ struct alignas(16) Smem {
   unsigned long long cnt_parents, cnt_children, cnt_probes;
   unsigned long long bcast;
   uint32_t hstep[6];  // a helper's view of the posted step
+  uint32_t multi_item;  // some parent of the step has other than one item
   uint32_t w_children, w_probes;
 };
 // rank scratch aliases the row arrays (used after expansion only)
@@ -684,6 +685,11 @@ struct StepView {
   double lnf_next;
   float tok_thr;
   double sent_thr;
+  // a solo step whose `next` pushes (at most this many) all survive keeps
+  // them in LDS: no flush, the leader emits from the push buffer
+  uint32_t keep_lds_max;
+  // every parent has exactly one work item (item w belongs to parent w)
+  bool one_each;
 };
 
 // Expands the step's work items: each is (parent, child) for a scanned
@@ -734,10 +740,14 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
     if (w < W) {
       // parent of work item w: the last j with woff[j] <= w
       uint32_t lo = 0, hi = v.n_par;
-      while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        const uint32_t o = lds_par ? sm.woff[mid] : ld_relaxed(&v.woff[mid]);
-        if (o <= w) lo = mid; else hi = mid;
+      if (v.one_each) {
+        lo = w;
+      } else {
+        while (hi - lo > 1) {
+          const uint32_t mid = (lo + hi) >> 1;
+          const uint32_t o = lds_par ? sm.woff[mid] : ld_relaxed(&v.woff[mid]);
+          if (o <= w) lo = mid; else hi = mid;
+        }
       }
       pj = lo;
       uint32_t md, c0, aux, q;
@@ -898,7 +908,8 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
     }
   }
   __syncthreads();
-  for (uint32_t i = tid; i < nl; i += kBlock) {
+  const bool next_in_lds = solo && sm.lq_next <= v.keep_lds_max;
+  for (uint32_t i = tid; i < (next_in_lds ? 0u : nl); i += kBlock) {
     const uint32_t o = sm.gb_next + i;
     const NextRec& r = sm.push_next[i];
     if (o < v.next_cap) st_next(&v.nextc[o], r.key, r.node, r.jk);
@@ -910,13 +921,10 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
 }
 
 // Loads the proposal row of step t (staged in ascending token order) into
-// LDS, and empties the row hash when the row is small enough to be hashed.
+// LDS.
 __device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
                          uint32_t t, uint32_t K, Smem& sm) {
   const uint64_t o = (uint64_t)t * K;
-  if (K <= kRowHashMaxK)
-    for (uint32_t i = threadIdx.x; i < (uint32_t)kRowHash; i += kBlock)
-      sm.rh_tok[i] = kRowHashEmpty;
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
     sm.row_id[p] = rid[o + p];
     sm.row_lp[p] = rlp[o + p];
@@ -929,6 +937,9 @@ __device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, 
 // Row tokens are distinct (staging rejects duplicates) and fill at most half
 // the table, so every insert ends in a free slot.  Ends synchronised.
 __device__ __forceinline__ void hash_row(uint32_t K, Smem& sm) {
+  for (uint32_t i = threadIdx.x; i < (uint32_t)kRowHash; i += kBlock)
+    sm.rh_tok[i] = kRowHashEmpty;
+  __syncthreads();
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
     const uint32_t tok = sm.row_id[p];
     if (tok >= kTokMask) continue;
@@ -1009,6 +1020,8 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.lnf_next = lnf[t + 1];
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
+    sv.keep_lds_max = 0;
+    sv.one_each = false;
     load_row(rid, rlp, rk, t, d.K, sm);
     __syncthreads();
     const bool hashed = d.K <= kRowHashMaxK;
@@ -1082,6 +1095,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   if (tid == 0) {
     st_cur(&cur[0], 0.0, 0, kNoHist);
     sm.status = 0;
+    sm.multi_item = 0;
     sm.cnt_parents = sm.cnt_children = sm.cnt_probes = 0;
   }
   uint32_t n_cur = 1, nS = 0, hist_used = 0;
@@ -1158,6 +1172,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       if (j < n_cur) {
         st_dev(&par_woff[j], W + off);
         if (n_cur <= (uint32_t)kBlock) sm.woff[j] = W + off;
+        if (work != 1) sm.multi_item = 1;  // cleared before the step began
       }
       W += Wc;
     }
@@ -1187,6 +1202,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     sv.lnf_next = lnf_next;
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
+    sv.keep_lds_max = min((uint32_t)kPushCap, beams[t]);
+    sv.one_each = n_cur <= (uint32_t)kBlock && sm.multi_item == 0;
 
     const bool shared = a.wgs > 1 && W >= a.share_min;
     if (shared) {
@@ -1391,9 +1408,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       __syncthreads();
       break;
     }
+    // a solo step whose pushes all survive left them in LDS (expand_range
+    // skipped their flush under the same condition)
+    const bool next_in_lds = !shared && n_next <= min((uint32_t)kPushCap, Mnext);
     // survivor i becomes hypothesis o of the next beam
     auto emit = [&](uint32_t i, uint32_t o) {
-      const NextRec c = nextc[i];
+      const NextRec c = next_in_lds ? sm.push_next[i] : nextc[i];
       const uint32_t j = c.jk >> 16, q = c.jk & 0xFFFFu;
       const CurRec p = cur[j];
       st_cur(&cur2[o], p.s + (double)rlp[(uint64_t)t * K + q], c.node, hist_used + o);
@@ -1472,6 +1492,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       cur_which ^= 1u;
     }
     t_sel += wall_clock64() - t1;
+    if (tid == 0) sm.multi_item = 0;  // for the next step's parent table
     __syncthreads();
   }
   // release the helpers
