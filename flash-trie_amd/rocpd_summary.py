@@ -12,9 +12,10 @@ its batch sizes with one launch of a different grid).
 
 With --pmc it prints, per kernel, grid size and counter, the mean value per
 dispatch of the counters a `rocprofv3 --pmc` run collected (FETCH_SIZE and
-WRITE_SIZE are in KiB).
+WRITE_SIZE are in KiB); with --pmc --runs, per run of consecutive dispatches
+(in dispatch order) that share kernel and grid size.
 
-Usage: python flash-trie_amd/rocpd_summary.py [--runs|--pmc] <results.db> [name-filter]
+Usage: python flash-trie_amd/rocpd_summary.py [--runs] [--pmc] <results.db> [name-filter]
 """
 
 import sqlite3
@@ -70,19 +71,26 @@ def run_summary(db, name_filter=""):
     return out
 
 
-def pmc_summary(db, name_filter=""):
+def pmc_summary(db, name_filter="", runs=False):
     con = sqlite3.connect(db)
     rows = con.execute(
         "select kernel_name, grid_size, workgroup_size, counter_name, value "
-        "from counters_collection").fetchall()
+        "from counters_collection order by dispatch_id").fetchall()
     groups = {}
+    order = []
     for name, grid, wg, counter, value in rows:
         if name_filter and name_filter not in name:
             continue
         key = (name, grid // max(wg, 1), counter)
-        groups.setdefault(key, []).append(value)
+        if runs:
+            if not order or order[-1][0] != key:
+                order.append((key, []))
+            order[-1][1].append(value)
+        else:
+            groups.setdefault(key, []).append(value)
+    items = ([(k, v) for k, v in order] if runs else sorted(groups.items()))
     out = []
-    for (name, wgs, counter), v in sorted(groups.items()):
+    for (name, wgs, counter), v in items:
         v = np.array(v, dtype=np.float64)
         out.append({"kernel": name, "workgroups": wgs, "counter": counter,
                     "dispatches": v.size, "mean": v.mean(), "min": v.min(),
@@ -96,7 +104,7 @@ def main():
         print(__doc__)
         sys.exit(1)
     if "--pmc" in sys.argv:
-        res = pmc_summary(args[0], args[1] if len(args) > 1 else "")
+        res = pmc_summary(args[0], args[1] if len(args) > 1 else "", "--runs" in sys.argv)
         print(f"{'kernel':<40} {'WGs':>5} {'counter':<12} {'dispatches':>10} "
               f"{'mean':>14} {'min':>14} {'max':>14}")
         for r in res:
