@@ -65,20 +65,21 @@ struct alignas(16) Smem {
   // expansion: the current proposal row in ascending token order
   uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
-  uint16_t row_k[kMaxLdsTopk];
+  // expansion: the parent table of up to kBlock parents (LDS copy): the
+  // work-item prefix, first child / table, degree / token / table size,
+  // node, lookup mode, score and history record.  Not aliased: the emit of
+  // a step writes the next step's table while the selection's arrays are
+  // still read.
+  uint32_t woff[kBlock + 1];
+  uint32_t p_c0[kBlock];
+  uint32_t p_aux[kBlock];
+  uint32_t p_node[kBlock];
+  uint32_t p_hist[kBlock];
+  double p_s[kBlock];
+  uint8_t p_mode[kBlock];
   union {
-    // expansion: the parent table of up to kBlock parents (LDS copy): the
-    // work-item prefix, first child / table, degree / token / table size,
-    // node, lookup mode, score and history record
+    // expansion: the row hash (see kRowHash)
     struct {
-      uint32_t woff[kBlock + 1];
-      uint32_t p_c0[kBlock];
-      uint32_t p_aux[kBlock];
-      uint32_t p_node[kBlock];
-      uint32_t p_hist[kBlock];
-      double p_s[kBlock];
-      uint8_t p_mode[kBlock];
-      // the row hash (see kRowHash)
       uint32_t rh_tok[kRowHash];
       uint16_t rh_pos[kRowHash];
     };
@@ -110,6 +111,7 @@ struct alignas(16) Smem {
   unsigned long long bcast;
   uint32_t hstep[6];  // a helper's view of the posted step
   uint32_t multi_item;  // some parent of the step has other than one item
+  uint32_t par_w;       // work items of a step with at most 64 parents
   uint32_t w_children, w_probes;
 };
 // rank scratch aliases the row arrays (used after expansion only)
@@ -185,25 +187,40 @@ __device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
   return base + lanemask_lt_count(m);
 }
 
+// Inclusive scan of x over the 64 lanes of a wave; every lane must be
+// active.  Lane moves are DPP operands of the adds (no LDS round trip):
+// shifts by 1, 2, 4, 8 within each row of 16 lanes, then lane 15 of each
+// row into the next row and lane 31 into the upper half.
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, Ctrl, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  const uint32_t lane = lane_id(), rl = lane & 15u;
+  uint32_t y = dpp_move<0x111>(x);  // row_shr:1
+  if (rl >= 1u) x += y;
+  y = dpp_move<0x112>(x);           // row_shr:2
+  if (rl >= 2u) x += y;
+  y = dpp_move<0x114>(x);           // row_shr:4
+  if (rl >= 4u) x += y;
+  y = dpp_move<0x118>(x);           // row_shr:8
+  if (rl >= 8u) x += y;
+  y = dpp_move<0x142>(x);           // row_bcast:15
+  if ((lane & 31u) >= 16u) x += y;
+  y = dpp_move<0x143>(x);           // row_bcast:31
+  if (lane >= 32u) x += y;
+  return x;
+}
+
 // Exclusive block scan of v over all kBlock threads.
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total, Smem& sm) {
   const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o, 64);
-    if (lane >= (uint32_t)o) x += y;
-  }
+  const uint32_t x = wave_incl_scan(v);
   if (lane == 63) sm.wsum[wave] = x;
   __syncthreads();
   if (wave == 0) {
-    uint32_t w = lane < (uint32_t)kWaves ? sm.wsum[lane] : 0;
-    uint32_t z = w;
-#pragma unroll
-    for (int o = 1; o < kWaves; o <<= 1) {
-      const uint32_t y = __shfl_up(z, o, 64);
-      if (lane >= (uint32_t)o) z += y;
-    }
+    const uint32_t w = lane < (uint32_t)kWaves ? sm.wsum[lane] : 0;
+    const uint32_t z = wave_incl_scan(w);
     if (lane < (uint32_t)kWaves) sm.wsum[lane] = z - w;  // exclusive
     if (lane == (uint32_t)kWaves - 1) sm.sel_cum = z;      // grand total
   }
@@ -578,6 +595,65 @@ __device__ __forceinline__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node
   return 0xFFFFFFFFu;
 }
 
+// A parent's entry in the parent table of step t: lookup mode (with
+// kModeDepthOk), first child or hash-table offset, degree / pending token /
+// log2 table size, and its number of work items.
+struct ParEntry {
+  uint32_t c0, aux, mode, work;
+};
+__device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, uint32_t t,
+                                                 uint32_t K, uint32_t* err) {
+  const ft_node_rec r = a.recs[node];
+  const uint32_t cend = a.recs[node + 1].child_begin;
+  const uint32_t deg = cend - r.child_begin;
+  const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
+  ParEntry e{r.child_begin, deg, (uint32_t)M_NONE, 0u};
+  if ((r.meta & FT_META_TERMINAL) && sd > t) {
+    // link parent: only KB(n)[|Q|] extends it (louds-trie.cc:91-102)
+    e.aux = kb_token(a, node, r, t, err);
+    e.mode = (t + 1 == sd) ? M_LP_SEL : M_LP_NEXT;
+    e.work = 1;
+  } else if (deg == 0) {
+    e.mode = M_NONE;
+  } else if (deg <= a.scan_limit) {
+    e.mode = M_SCAN;
+    e.work = deg;
+  } else {
+    e.mode = M_SEARCH;
+    e.work = K;
+    if (a.wdir && deg >= a.wide_min) {
+      // this node has a table: find it in the directory
+      const uint32_t mask = (1u << a.wdir_log2) - 1u;
+      uint32_t sl = fib_slot(node, a.wdir_log2);
+      for (uint32_t it = 0; it <= mask; ++it) {
+        const WideDir w = a.wdir[sl];
+        if (w.node == node) {
+          e.mode = M_HASH;
+          e.aux = w.log2nb;
+          e.c0 = w.bucket_off;
+          break;
+        }
+        if (w.node == kEmpty) break;
+        sl = (sl + 1) & mask;
+      }
+    }
+  }
+  if ((e.mode == M_SCAN || e.mode == M_HASH) && sd == t) e.mode |= kModeDepthOk;
+  return e;
+}
+
+// Work items of a parent-table entry.
+__device__ __forceinline__ uint32_t entry_work(uint32_t mode, uint32_t aux, uint32_t K) {
+  switch (mode & kModeMask) {
+    case M_LP_NEXT:
+    case M_LP_SEL: return 1u;
+    case M_SCAN: return aux;
+    case M_SEARCH:
+    case M_HASH: return K;
+    default: return 0u;
+  }
+}
+
 __device__ __forceinline__ uint32_t row_hash(uint32_t tok) {
   return (tok * 0x9E3779B1u) >> (32 - kRowHashLog2);
 }
@@ -710,25 +786,27 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
                              bool solo, bool hashed, Smem& sm) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const bool lds_par = v.n_par <= (uint32_t)kBlock;
-  if (lds_par && !par_in_lds) {
-    for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = ld_relaxed(&v.woff[i]);
-    for (uint32_t i = tid; i < v.n_par; i += kBlock) {
-      sm.p_c0[i] = ld_relaxed(&v.pc0[i]);
-      sm.p_aux[i] = ld_relaxed(&v.paux[i]);
-      sm.p_node[i] = ld_relaxed(&v.pnode[i]);
-      sm.p_mode[i] = (uint8_t)ld_relaxed(&v.pmode[i]);
-      const CurRec p = ld_cur(&v.cur[i]);
-      sm.p_s[i] = p.s;
-      sm.p_hist[i] = p.hist;
+  if (!par_in_lds) {
+    if (lds_par) {
+      for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = ld_relaxed(&v.woff[i]);
+      for (uint32_t i = tid; i < v.n_par; i += kBlock) {
+        sm.p_c0[i] = ld_relaxed(&v.pc0[i]);
+        sm.p_aux[i] = ld_relaxed(&v.paux[i]);
+        sm.p_node[i] = ld_relaxed(&v.pnode[i]);
+        sm.p_mode[i] = (uint8_t)ld_relaxed(&v.pmode[i]);
+        const CurRec p = ld_cur(&v.cur[i]);
+        sm.p_s[i] = p.s;
+        sm.p_hist[i] = p.hist;
+      }
     }
+    if (tid == 0) {
+      sm.w_children = 0;
+      sm.w_probes = 0;
+      sm.lq_next = 0;
+      sm.lq_sel = 0;
+    }
+    __syncthreads();
   }
-  if (tid == 0) {
-    sm.w_children = 0;
-    sm.w_probes = 0;
-    sm.lq_next = 0;
-    sm.lq_sel = 0;
-  }
-  __syncthreads();
   uint32_t my_children = 0, my_probes = 0;
   const uint32_t K = v.K, t = v.t;
   const uint32_t nchunks = (W + 63u) >> 6;
@@ -893,42 +971,42 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
   if (my_children) atomicAdd(&sm.w_children, my_children);
   if (my_probes) atomicAdd(&sm.w_probes, my_probes);
   __syncthreads();
-  // the buffered pushes: one global append per list
+  // the buffered pushes: one global append per list (a solo workgroup's
+  // lists start at 0)
   const uint32_t nl = min(sm.lq_next, (uint32_t)kPushCap);
   const uint32_t sl = min(sm.lq_sel, (uint32_t)kPushSelCap);
-  if (tid == 0) {
-    if (solo) {
-      sm.gb_next = 0;
-      sm.gb_sel = 0;
-    } else {
+  uint32_t gb_next = 0, gb_sel = 0;
+  if (!solo) {
+    if (tid == 0) {
       if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
       if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
       sm.gb_next = nl ? atomicAdd(&v.ctl->n_next, nl) : 0u;
       sm.gb_sel = sl ? atomicAdd(&v.ctl->n_sel, sl) : 0u;
     }
+    __syncthreads();
+    gb_next = sm.gb_next;
+    gb_sel = sm.gb_sel;
   }
-  __syncthreads();
   const bool next_in_lds = solo && sm.lq_next <= v.keep_lds_max;
   for (uint32_t i = tid; i < (next_in_lds ? 0u : nl); i += kBlock) {
-    const uint32_t o = sm.gb_next + i;
+    const uint32_t o = gb_next + i;
     const NextRec& r = sm.push_next[i];
     if (o < v.next_cap) st_next(&v.nextc[o], r.key, r.node, r.jk);
   }
   for (uint32_t i = tid; i < sl; i += kBlock) {
-    const uint32_t o = sm.gb_sel + i;
+    const uint32_t o = gb_sel + i;
     if (v.nS + o < v.sel_cap) st_sel(&v.sel[v.nS + o], sm.push_sel[i]);
   }
 }
 
 // Loads the proposal row of step t (staged in ascending token order) into
 // LDS.
-__device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, const uint16_t* rk,
-                         uint32_t t, uint32_t K, Smem& sm) {
+__device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, uint32_t t,
+                                         uint32_t K, Smem& sm) {
   const uint64_t o = (uint64_t)t * K;
   for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
     sm.row_id[p] = rid[o + p];
     sm.row_lp[p] = rlp[o + p];
-    sm.row_k[p] = rk[o + p];
   }
 }
 
@@ -967,7 +1045,6 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
   const double* lnf = (const double*)in;
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
   const float* rlp = (const float*)(in + d.rlp_off);
-  const uint16_t* rk = (const uint16_t*)(in + d.rk_off);
   for (;;) {
     if (tid == 0) {
       unsigned long long v = 0;
@@ -1022,7 +1099,7 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.sent_thr = d.sent_thr;
     sv.keep_lds_max = 0;
     sv.one_each = false;
-    load_row(rid, rlp, rk, t, d.K, sm);
+    load_row(rid, rlp, t, d.K, sm);
     __syncthreads();
     const bool hashed = d.K <= kRowHashMaxK;
     if (hashed) hash_row(d.K, sm);
@@ -1100,88 +1177,102 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   }
   uint32_t n_cur = 1, nS = 0, hist_used = 0;
   uint64_t n_cands = 0;
+  // the parent table of the step was written by the previous step's emit,
+  // and its row loaded into registers there (pf_*)
+  bool par_ready = false, row_pf = false;
+  uint32_t pf_id = 0;
+  float pf_lp = 0.0f;
   __syncthreads();
 
   for (uint32_t t = 0; t < T; ++t) {
     if (n_cur == 0 || (early && nS >= F)) break;
     const unsigned long long t0 = wall_clock64();
     const uint32_t ncur0 = n_cur;
-    load_row(rid, rlp, rk, t, K, sm);
+    if (row_pf) {
+      if (tid < K) {
+        sm.row_id[tid] = pf_id;
+        sm.row_lp[tid] = pf_lp;
+      }
+    } else {
+      load_row(rid, rlp, t, K, sm);
+    }
     const double lnf_next = lnf[t + 1];
 
     // ---- parents: lookup mode, work items, exclusive prefix ---------------
+    // work items of parent j (j < n_cur), writing its table entry unless the
+    // previous step's emit did
+    auto parent_work = [&](uint32_t j) -> uint32_t {
+      if (par_ready) {
+        const bool lp = n_cur <= (uint32_t)kBlock;
+        return entry_work(lp ? sm.p_mode[j] : ld_relaxed(&par_mode[j]),
+                          lp ? sm.p_aux[j] : ld_relaxed(&par_aux[j]), K);
+      }
+      const CurRec p = cur[j];
+      uint32_t err = 0;
+      const ParEntry e = parent_entry(a, p.node, t, K, &err);
+      if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
+      st_dev(&par_c0[j], e.c0);
+      st_dev(&par_aux[j], e.aux);
+      st_dev(&par_node[j], p.node);
+      st_dev(&par_mode[j], e.mode);
+      if (n_cur <= (uint32_t)kBlock) {
+        sm.p_c0[j] = e.c0;
+        sm.p_aux[j] = e.aux;
+        sm.p_node[j] = p.node;
+        sm.p_mode[j] = (uint8_t)e.mode;
+        sm.p_s[j] = p.s;
+        sm.p_hist[j] = p.hist;
+      }
+      return e.work;
+    };
     uint32_t W = 0;
-    for (uint32_t cbase = 0; cbase < n_cur; cbase += kBlock) {
-      const uint32_t j = cbase + tid;
-      uint32_t work = 0;
-      if (j < n_cur) {
-        const CurRec p = cur[j];
-        const ft_node_rec r = a.recs[p.node];
-        const uint32_t cend = a.recs[p.node + 1].child_begin;
-        const uint32_t deg = cend - r.child_begin;
-        const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
-        uint32_t aux = deg, pc0 = r.child_begin, mode = M_NONE;
-        if ((r.meta & FT_META_TERMINAL) && sd > t) {
-          // link parent: only KB(n)[|Q|] extends it (louds-trie.cc:91-102)
-          uint32_t err = 0;
-          aux = kb_token(a, p.node, r, t, &err);
-          if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
-          mode = (t + 1 == sd) ? M_LP_SEL : M_LP_NEXT;
-          work = 1;
-        } else if (deg == 0) {
-          mode = M_NONE;
-        } else if (deg <= a.scan_limit) {
-          mode = M_SCAN;
-          work = deg;
-        } else {
-          mode = M_SEARCH;
-          work = K;
-          if (a.wdir && deg >= a.wide_min) {
-            // this node has a table: find it in the directory
-            const uint32_t mask = (1u << a.wdir_log2) - 1u;
-            uint32_t sl = fib_slot(p.node, a.wdir_log2);
-            for (uint32_t it = 0; it <= mask; ++it) {
-              const WideDir e = a.wdir[sl];
-              if (e.node == p.node) {
-                mode = M_HASH;
-                aux = e.log2nb;
-                pc0 = e.bucket_off;
-                break;
-              }
-              if (e.node == kEmpty) break;
-              sl = (sl + 1) & mask;
-            }
-          }
+    const bool one_wave = n_cur <= 64u;
+    if (one_wave) {
+      // one wave holds every parent: its scan needs no barrier
+      if (tid < 64u) {
+        const uint32_t work = tid < n_cur ? parent_work(tid) : 0u;
+        const uint32_t incl = wave_incl_scan(work);
+        const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+        if (tid < n_cur) {
+          st_dev(&par_woff[tid], incl - work);
+          sm.woff[tid] = incl - work;
+          if (work != 1) sm.multi_item = 1;  // cleared before the step began
         }
-        if ((mode == M_SCAN || mode == M_HASH) && sd == t) mode |= kModeDepthOk;
-        st_dev(&par_c0[j], pc0);
-        st_dev(&par_aux[j], aux);
-        st_dev(&par_node[j], p.node);
-        st_dev(&par_mode[j], mode);
-        if (n_cur <= (uint32_t)kBlock) {
-          sm.p_c0[j] = pc0;
-          sm.p_aux[j] = aux;
-          sm.p_node[j] = p.node;
-          sm.p_mode[j] = (uint8_t)mode;
-          sm.p_s[j] = p.s;
-          sm.p_hist[j] = p.hist;
+        if (tid == 0) {
+          st_dev(&par_woff[n_cur], tot);
+          sm.woff[n_cur] = tot;
+          sm.par_w = tot;
         }
       }
-      uint32_t Wc;
-      const uint32_t off = block_excl_scan(work, &Wc, sm);
-      if (j < n_cur) {
-        st_dev(&par_woff[j], W + off);
-        if (n_cur <= (uint32_t)kBlock) sm.woff[j] = W + off;
-        if (work != 1) sm.multi_item = 1;  // cleared before the step began
+    } else {
+      for (uint32_t cbase = 0; cbase < n_cur; cbase += kBlock) {
+        const uint32_t j = cbase + tid;
+        const uint32_t work = j < n_cur ? parent_work(j) : 0u;
+        uint32_t Wc;
+        const uint32_t off = block_excl_scan(work, &Wc, sm);
+        if (j < n_cur) {
+          st_dev(&par_woff[j], W + off);
+          if (n_cur <= (uint32_t)kBlock) sm.woff[j] = W + off;
+          if (work != 1) sm.multi_item = 1;
+        }
+        W += Wc;
       }
-      W += Wc;
+      if (tid == 0) {
+        st_dev(&par_woff[n_cur], W);
+        if (n_cur <= (uint32_t)kBlock) sm.woff[n_cur] = W;
+      }
     }
     if (tid == 0) {
-      st_dev(&par_woff[n_cur], W);
-      if (n_cur <= (uint32_t)kBlock) sm.woff[n_cur] = W;
       sm.cnt_parents += n_cur;
+      // this workgroup's expansion counters (expand_range of the leader
+      // relies on them being zero)
+      sm.w_children = 0;
+      sm.w_probes = 0;
+      sm.lq_next = 0;
+      sm.lq_sel = 0;
     }
     __syncthreads();
+    if (one_wave) W = sm.par_w;
 
     StepView sv;
     sv.cur = cur;
@@ -1249,15 +1340,20 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     const uint32_t n_new = shared ? ld_relaxed(&ctl->n_sel) : sm.lq_sel;
     const unsigned long long w_ch = shared ? ld_relaxed(&ctl->children) : sm.w_children;
     const unsigned long long w_pr = shared ? ld_relaxed(&ctl->probes) : sm.w_probes;
-    __syncthreads();
+    // every writer of the status has passed the barrier above; only thread
+    // 0 adds the overflow bit below, which every thread derives itself
+    const bool overflow = n_next > next_cap || nS + n_new > sel_cap;
+    const bool stop = overflow || sm.status != 0;
     n_cands += (uint64_t)n_next + n_new;
     if (tid == 0) {
       sm.cnt_children += w_ch;
       sm.cnt_probes += w_pr;
-      if (n_next > next_cap || nS + n_new > sel_cap) sm.status |= kStatusOverflow;
+      if (overflow) sm.status |= kStatusOverflow;
     }
-    __syncthreads();
-    if (sm.status) break;
+    if (stop) {
+      __syncthreads();
+      break;
+    }
     const unsigned long long t1 = wall_clock64();
     t_exp += t1 - t0;
     if (tid == 0 && t < d.out_T) {
@@ -1323,7 +1419,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       auto sel_arr = [&](uint32_t i) {
         const SelRec& r = selA[i];
         if (!r.isnew) return 0u;
-        return 1u + rank[r.jk >> 16] * K + sm.row_k[r.jk & 0xFFFFu];
+        return 1u + rank[r.jk >> 16] * K + rk[(uint64_t)t * K + (r.jk & 0xFFFFu)];
       };
       auto sel_node = [&](uint32_t i) { return selA[i].node; };
       Bound b{0, 0, 0, 0, 1};
@@ -1345,7 +1441,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         b = bounded_select(nU, F, sel_key, sel_arr, sel_node, compute_ranks, sm);
       }
       if (b.all && !early_cut) {
-        // every push fits: the new items simply become old ones
+        // every push fits: the new items simply become old ones (no LDS
+        // state changed: no barrier)
         for (uint32_t i = nS + tid; i < nU; i += kBlock) st_dev(&selA[i].isnew, 0u);
         nS = nU;
       } else {
@@ -1374,8 +1471,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
           __syncthreads();
           break;
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
     if (stop_after) {
       t_sel += wall_clock64() - t1;
@@ -1387,7 +1484,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     auto nk = [&](uint32_t i) { return nextc[i].key; };
     auto na = [&](uint32_t i) {
       const uint32_t jk = nextc[i].jk;
-      return rank[jk >> 16] * K + sm.row_k[jk & 0xFFFFu];
+      return rank[jk >> 16] * K + rk[(uint64_t)t * K + (jk & 0xFFFFu)];
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
     const bool collect = M <= (uint32_t)kKeepCap;
@@ -1396,12 +1493,16 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
                                     nk_lo <= nk_hi, nk_lo, nk_hi, collect);
     // survivors already listed by the selection (keys above its boundary
     // bin), and the boundary bin's size
-    const bool listed = !bn.all && sm.collected != 0;
-    const uint32_t n_listed = min(sm.n_keep, (uint32_t)kKeepCap);
-    const uint32_t n_bin = min(sm.n_out, (uint32_t)kBinCap);
-    __syncthreads();
-    if (tid == 0) sm.n_out = 0;
-    __syncthreads();
+    bool listed = false;
+    uint32_t n_listed = 0, n_bin = 0;
+    if (!bn.all) {
+      listed = sm.collected != 0;
+      n_listed = min(sm.n_keep, (uint32_t)kKeepCap);
+      n_bin = min(sm.n_out, (uint32_t)kBinCap);
+      __syncthreads();
+      if (tid == 0) sm.n_out = 0;
+      __syncthreads();
+    }
     const uint32_t keep_cnt = bn.all ? n_next : M;
     if (hist_used + keep_cnt > hist_cap) {
       if (tid == 0) sm.status |= kStatusHistory;
@@ -1412,15 +1513,48 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // skipped their flush under the same condition)
     const bool next_in_lds = !shared && n_next <= min((uint32_t)kPushCap, Mnext);
     // survivor i becomes hypothesis o of the next beam
+    // the next step's proposal row, into registers while the survivors are
+    // emitted (the LDS row is still read until the emit ends)
+    row_pf = t + 1 < T && K <= (uint32_t)kBlock;
+    if (row_pf && tid < K) {
+      const uint64_t o = (uint64_t)(t + 1) * K + tid;
+      pf_id = rid[o];
+      pf_lp = rlp[o];
+    }
+    // The next step's parent table is filled here too: the node lookups of a
+    // survivor overlap the reads of its parent, and the next step starts
+    // with its table in place (in LDS as well when it has at most kBlock
+    // parents).
+    const bool next_table = t + 1 < T;
+    const bool next_lds = keep_cnt <= (uint32_t)kBlock;
     auto emit = [&](uint32_t i, uint32_t o) {
       const NextRec c = next_in_lds ? sm.push_next[i] : nextc[i];
       const uint32_t j = c.jk >> 16, q = c.jk & 0xFFFFu;
       const CurRec p = cur[j];
-      st_cur(&cur2[o], p.s + (double)rlp[(uint64_t)t * K + q], c.node, hist_used + o);
+      ParEntry e{0u, 0u, (uint32_t)M_NONE, 0u};
+      uint32_t err = 0;
+      if (next_table) e = parent_entry(a, c.node, t + 1, K, &err);
+      const double s2 = p.s + (double)rlp[(uint64_t)t * K + q];
+      st_cur(&cur2[o], s2, c.node, hist_used + o);
       HistRec h;
       h.phist = p.hist;
       h.tok = rid[(uint64_t)t * K + q];
       hist[hist_used + o] = h;
+      if (next_table) {
+        if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
+        st_dev(&par_c0[o], e.c0);
+        st_dev(&par_aux[o], e.aux);
+        st_dev(&par_node[o], c.node);
+        st_dev(&par_mode[o], e.mode);
+        if (next_lds) {
+          sm.p_c0[o] = e.c0;
+          sm.p_aux[o] = e.aux;
+          sm.p_node[o] = c.node;
+          sm.p_mode[o] = (uint8_t)e.mode;
+          sm.p_s[o] = s2;
+          sm.p_hist[o] = hist_used + o;
+        }
+      }
     };
     if (bn.all) {
       // everything survives, in push order
@@ -1478,6 +1612,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         if (keep && o < a.lay.cur_cap && hist_used + o < hist_cap) emit(i, o);
       }
     }
+    if (tid == 0) sm.multi_item = 0;  // for the next step's parent table
+    // (also orders this step's LDS reads before the next step's writes)
     __syncthreads();
     n_cur = sm.n_out;
     if (tid == 0 && t < d.out_T) step_stats[(uint64_t)t * kStepStats + 5] = wall_clock64() - t1;
@@ -1491,9 +1627,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       CurRec* tmp = cur; cur = cur2; cur2 = tmp;
       cur_which ^= 1u;
     }
+    par_ready = next_table;
     t_sel += wall_clock64() - t1;
-    if (tid == 0) sm.multi_item = 0;  // for the next step's parent table
-    __syncthreads();
   }
   // release the helpers
   if (tid == 0) st_dev(&ctl->go, tag | kGoExit);
