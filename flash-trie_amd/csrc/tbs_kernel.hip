@@ -62,8 +62,26 @@ constexpr uint32_t kRowHashEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kRowHashMinWork = 2048;
 
 struct alignas(16) Smem {
+  // counters, flags and small arrays first: their LDS addresses fit the
+  // immediate offset of one base register
+  // expansion: this workgroup's push counts and list bases
+  uint32_t lq_next, lq_sel, gb_next, gb_sel;
+  // selection
+  uint32_t hist[256];
+  uint64_t red64[2 * kWaves];
+  uint32_t wsum[kWaves];
+  uint32_t sel_digit, sel_cum, sel_cnt;
+  uint32_t n_keep, collected;
+  uint32_t n_next, n_sel, n_out, overflow;
+  uint32_t status;
+  unsigned long long cnt_parents, cnt_children, cnt_probes;
+  unsigned long long bcast;
+  uint32_t hstep[6];  // a helper's view of the posted step
+  uint32_t multi_item;  // some parent of the step has other than one item
+  uint32_t par_w;       // work items of a step with at most 64 parents
+  uint32_t w_children, w_probes;
   // expansion: the current proposal row in ascending token order
-  uint32_t row_id[kMaxLdsTopk];
+  alignas(16) uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
   // expansion: the parent table of up to kBlock parents (LDS copy): the
   // work-item prefix, first child / table, degree / token / table size,
@@ -77,6 +95,18 @@ struct alignas(16) Smem {
   uint32_t p_hist[kBlock];
   double p_s[kBlock];
   uint8_t p_mode[kBlock];
+  // link parents (kNoCursor otherwise): index in tail[] of the pending token
+  uint32_t p_lp[kBlock];
+  // the leader's own per-parent data for its emit, which overwrites the
+  // table above with the next step's, copied by the parent phase: score,
+  // history record and, for a link parent that stays one on its own edge,
+  // its string depth (else 0) and the tail index of its pending token; the
+  // expansion of that parent adds its next pending token (else kNoToken)
+  double x_s[kBlock];
+  uint32_t x_hist[kBlock];
+  uint32_t x_tok[kBlock];
+  uint32_t x_tc[kBlock];
+  uint16_t x_sd[kBlock];
   union {
     // expansion: the row hash (see kRowHash)
     struct {
@@ -97,22 +127,6 @@ struct alignas(16) Smem {
   // the end of its share of the step
   NextRec push_next[kPushCap];
   SelRec push_sel[kPushSelCap];
-  uint32_t lq_next, lq_sel, gb_next, gb_sel;
-  // selection
-  uint32_t hist[256];
-  uint64_t red64[2 * kWaves];
-
-  uint32_t wsum[kWaves];
-  uint32_t sel_digit, sel_cum, sel_cnt;
-  uint32_t n_keep, collected;
-  uint32_t n_next, n_sel, n_out, overflow;
-  uint32_t status;
-  unsigned long long cnt_parents, cnt_children, cnt_probes;
-  unsigned long long bcast;
-  uint32_t hstep[6];  // a helper's view of the posted step
-  uint32_t multi_item;  // some parent of the step has other than one item
-  uint32_t par_w;       // work items of a step with at most 64 parents
-  uint32_t w_children, w_probes;
 };
 // rank scratch aliases the row arrays (used after expansion only)
 constexpr int kRankChunk = 1024;
@@ -596,10 +610,14 @@ __device__ __forceinline__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node
 }
 
 // A parent's entry in the parent table of step t: lookup mode (with
-// kModeDepthOk), first child or hash-table offset, degree / pending token /
-// log2 table size, and its number of work items.
+// kModeDepthOk), first child or hash-table offset (a link parent: its string
+// depth), degree / pending token / log2 table size, its number of work
+// items, and for a link parent whose pending token lies on its own edge the
+// index of that token in tail[] (else kNoCursor).
+constexpr uint32_t kNoCursor = 0xFFFFFFFFu;
+constexpr uint32_t kNoToken = 0xFFFFFFFFu;
 struct ParEntry {
-  uint32_t c0, aux, mode, work;
+  uint32_t c0, aux, mode, work, lp;
 };
 __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, uint32_t t,
                                                  uint32_t K, uint32_t* err) {
@@ -607,12 +625,15 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
   const uint32_t cend = a.recs[node + 1].child_begin;
   const uint32_t deg = cend - r.child_begin;
   const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
-  ParEntry e{r.child_begin, deg, (uint32_t)M_NONE, 0u};
+  ParEntry e{r.child_begin, deg, (uint32_t)M_NONE, 0u, kNoCursor};
   if ((r.meta & FT_META_TERMINAL) && sd > t) {
     // link parent: only KB(n)[|Q|] extends it (louds-trie.cc:91-102)
     e.aux = kb_token(a, node, r, t, err);
     e.mode = (t + 1 == sd) ? M_LP_SEL : M_LP_NEXT;
     e.work = 1;
+    e.c0 = sd;
+    const uint32_t el = (r.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+    if ((r.meta & FT_META_LINK) && t + el >= sd) e.lp = r.tail_off + (t + el - sd);
   } else if (deg == 0) {
     e.mode = M_NONE;
   } else if (deg <= a.scan_limit) {
@@ -843,11 +864,18 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
       const bool depth_ok = (md & kModeDepthOk) != 0;
       md &= kModeMask;
       int pos = -1;
-      ft_node_rec cr;
       bool have_child = false, label_sel = false;
       if (md == M_LP_NEXT || md == M_LP_SEL) {
+        // the leader reads the next pending token of a link parent that
+        // stays one (for its emit) while the row is searched
+        uint32_t xtok = kNoToken;
+        if (par_in_lds && lds_par && md == M_LP_NEXT) {
+          const uint32_t tc = sm.p_lp[pj];
+          if (tc != kNoCursor) xtok = a.tail[tc + 1u];
+        }
         pos = row_find(sm, K, aux, hashed);
         cnode = lds_par ? sm.p_node[pj] : ld_relaxed(&v.pnode[pj]);
+        if (xtok != kNoToken) sm.x_tok[pj] = xtok;
       } else if (md == M_SCAN) {
         // the child's label: its first token, and whether it closes a key
         cnode = c0 + q;
@@ -879,10 +907,13 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
               if (a.recs[mid].first_tok < tok) lo2 = mid + 1; else hi2 = mid;
             }
             if (lo2 < end2) {
-              cr = a.recs[lo2];
+              const ft_node_rec cr = a.recs[lo2];
               if (cr.first_tok == tok) {
                 cnode = lo2;
                 have_child = true;
+                // terminal with |KB| == |Q| -> selected (louds-trie.cc:103-108)
+                label_sel = (cr.meta & FT_META_TERMINAL) &&
+                            (cr.meta & FT_META_DEPTH_MASK) == t + 1;
               }
             }
           } else if (md == M_HASH) {
@@ -921,13 +952,10 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
           } else if (md == M_LP_SEL) {
             do_sel = true;
           } else if (have_child) {
-            // terminal with |KB| == |Q| -> selected; always next
-            // (louds-trie.cc:103-108)
+            // a child is always next; selected when it closes a key of
+            // length t + 1 (louds-trie.cc:103-108)
             do_next = true;
-            do_sel = (md == M_SEARCH)
-                         ? ((cr.meta & FT_META_TERMINAL) &&
-                            (cr.meta & FT_META_DEPTH_MASK) == t + 1)
-                         : label_sel;
+            do_sel = label_sel;
           }
         }
       }
@@ -1202,10 +1230,18 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // work items of parent j (j < n_cur), writing its table entry unless the
     // previous step's emit did
     auto parent_work = [&](uint32_t j) -> uint32_t {
+      const bool lp = n_cur <= (uint32_t)kBlock;
       if (par_ready) {
-        const bool lp = n_cur <= (uint32_t)kBlock;
-        return entry_work(lp ? sm.p_mode[j] : ld_relaxed(&par_mode[j]),
-                          lp ? sm.p_aux[j] : ld_relaxed(&par_aux[j]), K);
+        if (lp) {
+          const uint32_t md = sm.p_mode[j], c0 = sm.p_c0[j], cur_lp = sm.p_lp[j];
+          sm.x_s[j] = sm.p_s[j];
+          sm.x_hist[j] = sm.p_hist[j];
+          sm.x_sd[j] = (md == M_LP_NEXT && cur_lp != kNoCursor) ? (uint16_t)c0 : (uint16_t)0;
+          sm.x_tc[j] = cur_lp;
+          sm.x_tok[j] = kNoToken;
+          return entry_work(md, sm.p_aux[j], K);
+        }
+        return entry_work(ld_relaxed(&par_mode[j]), ld_relaxed(&par_aux[j]), K);
       }
       const CurRec p = cur[j];
       uint32_t err = 0;
@@ -1215,13 +1251,19 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       st_dev(&par_aux[j], e.aux);
       st_dev(&par_node[j], p.node);
       st_dev(&par_mode[j], e.mode);
-      if (n_cur <= (uint32_t)kBlock) {
+      if (lp) {
         sm.p_c0[j] = e.c0;
         sm.p_aux[j] = e.aux;
         sm.p_node[j] = p.node;
         sm.p_mode[j] = (uint8_t)e.mode;
+        sm.p_lp[j] = e.lp;
         sm.p_s[j] = p.s;
         sm.p_hist[j] = p.hist;
+        sm.x_s[j] = p.s;
+        sm.x_hist[j] = p.hist;
+        sm.x_sd[j] = (e.mode == M_LP_NEXT && e.lp != kNoCursor) ? (uint16_t)e.c0 : (uint16_t)0;
+        sm.x_tc[j] = e.lp;
+        sm.x_tok[j] = kNoToken;
       }
       return e.work;
     };
@@ -1527,18 +1569,48 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // parents).
     const bool next_table = t + 1 < T;
     const bool next_lds = keep_cnt <= (uint32_t)kBlock;
+    // the parents' scores and history records, and their link tokens, are
+    // in LDS when the step had at most kBlock parents; the row is, unless
+    // the rank scratch took it
+    const bool x_ok = ncur_now <= (uint32_t)kBlock;
+    const bool row_ok = !ranks_done;
     auto emit = [&](uint32_t i, uint32_t o) {
       const NextRec c = next_in_lds ? sm.push_next[i] : nextc[i];
       const uint32_t j = c.jk >> 16, q = c.jk & 0xFFFFu;
-      const CurRec p = cur[j];
-      ParEntry e{0u, 0u, (uint32_t)M_NONE, 0u};
+      double ps;
+      uint32_t phist;
+      if (x_ok) {
+        ps = sm.x_s[j];
+        phist = sm.x_hist[j];
+      } else {
+        const CurRec p = cur[j];
+        ps = p.s;
+        phist = p.hist;
+      }
+      const float x = row_ok ? sm.row_lp[q] : rlp[(uint64_t)t * K + q];
+      const uint32_t tk = row_ok ? sm.row_id[q] : rid[(uint64_t)t * K + q];
+      ParEntry e{0u, 0u, (uint32_t)M_NONE, 0u, kNoCursor};
       uint32_t err = 0;
-      if (next_table) e = parent_entry(a, c.node, t + 1, K, &err);
-      const double s2 = p.s + (double)rlp[(uint64_t)t * K + q];
+      if (next_table) {
+        const uint32_t xtok = x_ok ? sm.x_tok[j] : kNoToken;
+        if (xtok != kNoToken) {
+          // a link parent that stays one, on its own edge: the entry
+          // parent_entry() would build, from what its expansion read
+          const uint32_t xsd = sm.x_sd[j];
+          e.c0 = xsd;
+          e.aux = xtok;
+          e.mode = (t + 2 == xsd) ? M_LP_SEL : M_LP_NEXT;
+          e.work = 1;
+          e.lp = sm.x_tc[j] + 1u;
+        } else {
+          e = parent_entry(a, c.node, t + 1, K, &err);
+        }
+      }
+      const double s2 = ps + (double)x;
       st_cur(&cur2[o], s2, c.node, hist_used + o);
       HistRec h;
-      h.phist = p.hist;
-      h.tok = rid[(uint64_t)t * K + q];
+      h.phist = phist;
+      h.tok = tk;
       hist[hist_used + o] = h;
       if (next_table) {
         if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
@@ -1551,19 +1623,23 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
           sm.p_aux[o] = e.aux;
           sm.p_node[o] = c.node;
           sm.p_mode[o] = (uint8_t)e.mode;
+          sm.p_lp[o] = e.lp;
           sm.p_s[o] = s2;
           sm.p_hist[o] = hist_used + o;
         }
       }
     };
+    // the survivors: all pushes in push order, or a list of positions in
+    // sm.keep_idx; then one emit loop (a list longer than kKeepCap is
+    // emitted as it is found)
+    uint32_t n_emit = 0;
+    bool from_list = false, list_done = true;
     if (bn.all) {
-      // everything survives, in push order
-      for (uint32_t i = tid; i < n_next; i += kBlock)
-        if (i < a.lay.cur_cap && hist_used + i < hist_cap) emit(i, i);
+      n_emit = n_next;
       if (tid == 0) sm.n_out = n_next;
     } else if (listed) {
       // the boundary bin's survivors join the listed ones (a record is read
-      // only for a key on the boundary of a cut tie), then the records
+      // only for a key on the boundary of a cut tie)
       if (tid == 0) sm.n_keep = n_listed;
       __syncthreads();
       for (uint32_t b = tid; b < n_bin + ((kBlock - n_bin % kBlock) % kBlock); b += kBlock) {
@@ -1579,14 +1655,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         if (keep && q < (uint32_t)kKeepCap) sm.keep_idx[q] = i;
       }
       __syncthreads();
-      const uint32_t nk2 = min(sm.n_keep, (uint32_t)kKeepCap);
-      for (uint32_t o = tid; o < nk2; o += kBlock)
-        if (o < a.lay.cur_cap && hist_used + o < hist_cap) emit(sm.keep_idx[o], o);
+      n_emit = min(sm.n_keep, (uint32_t)kKeepCap);
+      from_list = true;
       if (tid == 0) sm.n_out = sm.n_keep;
     } else if (keep_cnt <= (uint32_t)kKeepCap) {
       // positions of the survivors first (from the keys alone; the rest of
-      // a record is read only for a key on the boundary of a cut tie), then
-      // their records: one dependent chain per survivor
+      // a record is read only for a key on the boundary of a cut tie)
       visit_keys(n_next, nk, [&](uint32_t i, bool ok, uint64_t key) {
         bool keep = false;
         if (ok) {
@@ -1597,9 +1671,16 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         if (keep && o < (uint32_t)kKeepCap) sm.keep_idx[o] = i;
       });
       __syncthreads();
-      const uint32_t nk2 = min(sm.n_out, (uint32_t)kKeepCap);
-      for (uint32_t o = tid; o < nk2; o += kBlock)
-        if (o < a.lay.cur_cap && hist_used + o < hist_cap) emit(sm.keep_idx[o], o);
+      n_emit = min(sm.n_out, (uint32_t)kKeepCap);
+      from_list = true;
+    } else {
+      list_done = false;
+    }
+    if (list_done) {
+      // one dependent chain per survivor
+      for (uint32_t o = tid; o < n_emit; o += kBlock)
+        if (o < a.lay.cur_cap && hist_used + o < hist_cap)
+          emit(from_list ? sm.keep_idx[o] : o, o);
     } else {
       for (uint32_t base = 0; base < n_next; base += kBlock) {
         const uint32_t i = base + tid;
