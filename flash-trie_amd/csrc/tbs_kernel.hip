@@ -197,7 +197,7 @@ __device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
   const int leader = __ffsll((unsigned long long)m) - 1;
   uint32_t base = 0;
   if ((int)lane_id() == leader) base = atomicAdd(ctr, (uint32_t)__popcll(m));
-  base = __shfl(base, leader, 64);
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
   return base + lanemask_lt_count(m);
 }
 
@@ -252,7 +252,7 @@ __device__ __forceinline__ void hist_add(bool act, uint32_t digit,
   const uint64_t am = __ballot(act);
   if (am == 0) return;
   const int leader = __ffsll((unsigned long long)am) - 1;
-  const uint32_t d0 = __shfl(digit, leader, 64);
+  const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)digit, leader);
   const uint64_t same = __ballot(act && digit == d0);
   if (same == am) {
     if ((int)lane_id() == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(am));
@@ -269,12 +269,7 @@ __device__ __forceinline__ void hist_pick(uint32_t rem, Smem& sm) {
     const uint32_t h0 = sm.hist[4 * lane], h1 = sm.hist[4 * lane + 1],
                    h2 = sm.hist[4 * lane + 2], h3 = sm.hist[4 * lane + 3];
     const uint32_t own = h0 + h1 + h2 + h3;
-    uint32_t x = own;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(x, o, 64);
-      if (lane >= (uint32_t)o) x += y;
-    }
+    const uint32_t x = wave_incl_scan(own);
     const uint64_t hit = __ballot(x >= rem);
     const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
     if ((int)lane == first) {
@@ -333,16 +328,17 @@ __device__ __forceinline__ KeyT radix_kth(uint32_t n, uint32_t need, GetKey gk, 
 }
 
 // Calls f(i, valid, gk(i)) for every item slot i = base + tid of this
-// thread, with four items per thread in flight.
-template <typename GetKey, typename F>
+// thread (n >= 1 when the loop runs), with U items per thread in flight:
+// the reads are unconditional (a slot past the end re-reads item n - 1) so
+// that all of them are issued before the first is waited for.
+template <uint32_t U = 4, typename GetKey, typename F>
 __device__ __forceinline__ void visit_keys(uint32_t n, GetKey gk, F f) {
-  constexpr uint32_t U = 4;
   for (uint32_t base = 0; base < n; base += U * kBlock) {
     uint64_t k[U];
 #pragma unroll
     for (uint32_t u = 0; u < U; ++u) {
       const uint32_t i = base + u * kBlock + threadIdx.x;
-      k[u] = i < n ? gk(i) : 0;
+      k[u] = gk(min(i, n - 1u));
     }
 #pragma unroll
     for (uint32_t u = 0; u < U; ++u) {
@@ -420,7 +416,7 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
     const uint64_t hi_mask = (top >= 63) ? 0ull : ~((2ull << top) - 1ull);
     for (uint32_t i = tid; i < nb; i += kBlock) sm.whist[i] = 0;
     __syncthreads();
-    visit_keys(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+    visit_keys<8>(n, gk, [&](uint32_t, bool ok, uint64_t k) {
       const uint64_t o = k - base;
       const bool act = ok && (o & hi_mask) == prefix;
       hist_add(act, (uint32_t)((o >> sh) & (nb - 1)), sm.whist);
@@ -473,7 +469,7 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
       sm.collected = collect ? 1u : 0u;
     }
     __syncthreads();
-    visit_keys(n, gk, [&](uint32_t i, bool ok, uint64_t k) {
+    visit_keys<6>(n, gk, [&](uint32_t i, bool ok, uint64_t k) {
       const uint64_t hk = (k - base) & hi_mask;
       const bool act = ok && hk == prefix;
       const uint32_t o = wave_append(act, &sm.n_out);
