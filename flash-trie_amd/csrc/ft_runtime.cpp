@@ -76,6 +76,7 @@ struct ft_ctx {
   // wide-node index (device)
   WideDir* d_wdir = nullptr;
   WideBucket* d_wtab = nullptr;
+  uint64_t* d_wfp = nullptr;     // per bucket: slot fingerprints
   uint32_t* d_labels = nullptr;  // per node: first token | kSlotSel
   uint32_t wdir_log2 = 0, wide_min = 0;
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
@@ -294,6 +295,32 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
       });
     for (auto& x : th) x.join();
   }
+  // fingerprint words (every bucket, tables that failed included: they are
+  // cleared and never read), and the filter flag of small tables
+  std::unique_ptr<uint64_t[]> fpw(new (std::nothrow) uint64_t[buckets]);
+  if (!fpw) return fail(FT_E_NOMEM, "wide-node index: host memory");
+  {
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&, w]() {
+        const uint64_t b0 = buckets * w / T, b1 = buckets * (w + 1) / T;
+        for (uint64_t b = b0; b < b1; ++b) {
+          uint64_t f = 0;
+          for (uint32_t sl = 0; sl < kBucketSlots; ++sl) {
+            const uint32_t tw = tab[b].tok[sl];
+            if (tw != kSlotEmptyTok) f |= (uint64_t)wide_fp(tw & kTokMask) << (8 * sl);
+          }
+          fpw[b] = f;
+        }
+      });
+    for (auto& x : th) x.join();
+  }
+  uint32_t fp_max = kFpMaxLog2;
+  if (const char* fe = std::getenv("FT_FP_MAX_LOG2")) {
+    const long v = std::strtol(fe, nullptr, 10);
+    if (v >= 0 && v <= 32) fp_max = (uint32_t)v;
+  }
+  for (auto& e : ent) e.flags = e.log2nb <= fp_max ? kWideFiltered : 0u;
   uint64_t n_ok = 0;
   for (size_t i = 0; i < ent.size(); ++i) n_ok += failed[i] ? 0 : 1;
   uint32_t dlg = 1;
@@ -310,12 +337,17 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
     return hip_fail(e, "hipMalloc(wide dir)");
   if ((e = hipMalloc(&c->d_wtab, buckets * sizeof(WideBucket))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide tables)");
+  if ((e = hipMalloc(&c->d_wfp, buckets * sizeof(uint64_t))) != hipSuccess)
+    return hip_fail(e, "hipMalloc(wide fingerprints)");
   if ((e = hipMemcpy(c->d_wdir, dir.data(), dir.size() * sizeof(WideDir),
                      hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(e, "hipMemcpy(wide dir)");
   if ((e = hipMemcpy(c->d_wtab, tab.get(), buckets * sizeof(WideBucket),
                      hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(e, "hipMemcpy(wide tables)");
+  if ((e = hipMemcpy(c->d_wfp, fpw.get(), buckets * sizeof(uint64_t),
+                     hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy(wide fingerprints)");
   c->wdir_log2 = dlg;
   c->wide_min = (uint32_t)wmin;
   c->wide_nodes = n_ok;
@@ -716,6 +748,7 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   a.epoch = ep;
   a.wdir = c->d_wdir;
   a.wtab = c->d_wtab;
+  a.wfp = c->d_wfp;
   a.labels = c->d_labels;
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
@@ -871,6 +904,7 @@ void ft_destroy(ft_ctx* c) {
   if (c->d_image) (void)hipFree(c->d_image);
   if (c->d_wdir) (void)hipFree(c->d_wdir);
   if (c->d_wtab) (void)hipFree(c->d_wtab);
+  if (c->d_wfp) (void)hipFree(c->d_wfp);
   if (c->d_labels) (void)hipFree(c->d_labels);
   for (auto& ev : c->ring)
     if (ev) (void)hipEventDestroy(ev);

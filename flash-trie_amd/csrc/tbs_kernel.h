@@ -97,12 +97,22 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 // alone and read the child word of the matching slot only.  Tables are
 // found through a directory keyed by node id (Fibonacci hashing, linear
 // probing, node 0xFFFFFFFF marks an empty entry).
+//
+// Every bucket also has an 8-byte fingerprint word: byte s is
+// wide_fp(token) of slot s, 0 for an empty slot.  For a table of at most
+// 2^kFpMaxLog2 buckets (flag kWideFiltered), a lookup reads the fingerprint
+// word of h1(tok) first -- and of h2(tok) when that word is full -- and
+// reads no bucket when no byte matches: the token is not a child.  The
+// fingerprints of a small table are 1/8 of its bytes and stay cached across
+// the K lookups of a step, so most lookups (misses) cost no table read.
 struct WideDir {
   uint32_t node;
   uint32_t log2nb;      // log2 of the bucket count (>= 1)
   uint32_t bucket_off;  // first bucket of the node's table
-  uint32_t pad;
+  uint32_t flags;       // kWideFiltered
 };
+constexpr uint32_t kWideFiltered = 1u;
+constexpr uint32_t kFpMaxLog2 = 12;
 constexpr uint32_t kBucketSlots = 8;
 struct WideBucket {
   uint32_t tok[kBucketSlots];
@@ -118,6 +128,11 @@ __host__ __device__ inline uint32_t fib_slot(uint32_t x, uint32_t log2n) {
 }
 __host__ __device__ inline uint32_t cuckoo_h1(uint32_t tok, uint32_t lg) {
   return (tok * 0x9E3779B1u) >> (32 - lg);
+}
+// 8-bit token fingerprint in [1, 255] (0 marks an empty slot)
+__host__ __device__ inline uint32_t wide_fp(uint32_t tok) {
+  const uint32_t f = ((tok & 0x7FFFFFFFu) * 0x2545F491u) >> 24;
+  return f ? f : 1u;
 }
 __host__ __device__ inline uint32_t cuckoo_h2(uint32_t tok, uint32_t lg) {
   uint32_t h = (tok ^ 0x2545F491u) * 0x85EBCA6Bu;
@@ -166,6 +181,7 @@ struct KArgs {
   uint32_t scan_limit;
   const WideDir* wdir;   // null: no wide-node index
   const WideBucket* wtab;
+  const uint64_t* wfp;   // fingerprint word per bucket
   const uint32_t* labels;  // per node: first token | kSlotSel
   uint32_t wdir_log2;
   uint32_t wide_min;

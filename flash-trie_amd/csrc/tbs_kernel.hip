@@ -164,8 +164,10 @@ __device__ __forceinline__ uint32_t count_before(const uint64_t* rk_key,
 // lookup mode word of a parent: the mode, and whether the parent sits at
 // string depth t (only then can a child -- one token long, terminal --
 // close a key of length t + 1)
-constexpr uint32_t kModeMask = 0x7Fu;
+constexpr uint32_t kModeMask = 0x0Fu;
 constexpr uint32_t kModeDepthOk = 0x80u;
+// a hashed parent whose table has fingerprint filtering (kWideFiltered)
+constexpr uint32_t kModeFiltered = 0x40u;
 
 enum : uint8_t {
   M_NONE = 0,
@@ -184,6 +186,11 @@ __device__ __forceinline__ uint64_t norm_key(double v) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
+
+// whether some byte of v is zero
+__device__ __forceinline__ bool has_zero_byte(uint64_t v) {
+  return ((v - 0x0101010101010101ull) & ~v & 0x8080808080808080ull) != 0;
+}
 
 __device__ __forceinline__ uint32_t lanemask_lt_count(uint64_t m) {
   const uint32_t lane = lane_id();
@@ -645,7 +652,7 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
       for (uint32_t it = 0; it <= mask; ++it) {
         const WideDir w = a.wdir[sl];
         if (w.node == node) {
-          e.mode = M_HASH;
+          e.mode = M_HASH | ((w.flags & kWideFiltered) ? kModeFiltered : 0u);
           e.aux = w.log2nb;
           e.c0 = w.bucket_off;
           break;
@@ -655,7 +662,9 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
       }
     }
   }
-  if ((e.mode == M_SCAN || e.mode == M_HASH) && sd == t) e.mode |= kModeDepthOk;
+  if ((e.mode & kModeMask) == M_SCAN || (e.mode & kModeMask) == M_HASH) {
+    if (sd == t) e.mode |= kModeDepthOk;
+  }
   return e;
 }
 
@@ -858,6 +867,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
         aux = ld_relaxed(&v.paux[pj]);
       }
       const bool depth_ok = (md & kModeDepthOk) != 0;
+      const bool filtered = (md & kModeFiltered) != 0;
       md &= kModeMask;
       int pos = -1;
       bool have_child = false, label_sel = false;
@@ -917,8 +927,18 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
             // first is full without a match
             const uint32_t lg = aux;
             uint32_t b = c0 + cuckoo_h1(tok, lg);
+            // a filtered table: no fingerprint match in the first bucket
+            // (nor in the second, when the first is full) means no child
+            bool maybe = true;
+            if (filtered) {
+              const uint64_t f8 = (uint64_t)wide_fp(tok) * 0x0101010101010101ull;
+              const uint64_t w1 = a.wfp[b];
+              maybe = has_zero_byte(w1 ^ f8);
+              if (!maybe && !has_zero_byte(w1))
+                maybe = has_zero_byte(a.wfp[c0 + cuckoo_h2(tok, lg)] ^ f8);
+            }
             uint32_t hw = 0, hc = 0;
-            for (int round = 0; round < 2; ++round) {
+            for (int round = 0; round < (maybe ? 2 : 0); ++round) {
               // the whole bucket (tokens and children) in one read
               const uint4* bw = (const uint4*)&a.wtab[b];
               const uint4 ta = bw[0], tb = bw[1], ca = bw[2], cb = bw[3];

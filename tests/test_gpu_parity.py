@@ -242,13 +242,16 @@ def test_beam_1000(ft, po):
         assert_same_results((got[0][0], got[1][0]), want, f"B1000 {r}")
 
 
-@pytest.mark.parametrize("scan_mult,wide_min", [("0", "0"), ("0", "2"),
-                                                ("999999", "512"), ("1", "64")])
-def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min):
+@pytest.mark.parametrize("scan_mult,wide_min,fp_max", [
+    ("0", "0", "12"), ("0", "2", "12"), ("0", "2", "0"), ("999999", "512", "12"),
+    ("1", "64", "12"), ("1", "64", "0")])
+def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min, fp_max):
     # scan_mult 0 sends every parent with children to the binary search
-    # (wide_min 0) or the hash tables (wide_min 2); 999999 scans all
+    # (wide_min 0) or the hash tables (wide_min 2); 999999 scans all.
+    # fp_max 0 reads every hashed lookup's bucket (no fingerprint filter).
     monkeypatch.setenv("FT_SCAN_MULT", scan_mult)
     monkeypatch.setenv("FT_WIDE_MIN", wide_min)
+    monkeypatch.setenv("FT_FP_MAX_LOG2", fp_max)
     toks, offs = ft.synth_keys(50000, 4096, 3, 8, 1.1, 4)
     t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=32, steps=8,
                   beams=16, inter=2048)
@@ -264,7 +267,7 @@ def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min):
             want = o.tbs([16] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0,
                          b0 % 8 == 4)
             assert_same_results((got[0][i], got[1][i]), want,
-                                f"modes {scan_mult}/{wide_min} req {b0 + i}")
+                                f"modes {scan_mult}/{wide_min}/{fp_max} req {b0 + i}")
 
 
 @pytest.mark.parametrize("wgs,share_min", [("2", "0"), ("7", "0"), ("64", "0"),
