@@ -103,8 +103,9 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 // 2^kFpMaxLog2 buckets (flag kWideFiltered), a lookup reads the fingerprint
 // word of h1(tok) first -- and of h2(tok) when that word is full -- and
 // reads no bucket when no byte matches: the token is not a child.  The
-// fingerprints of a small table are 1/8 of its bytes and stay cached across
-// the K lookups of a step, so most lookups (misses) cost no table read.
+// fingerprints are 1/8 of a table's bytes (those of a small table stay
+// cached across the K lookups of a step), and most lookups are misses that
+// then read 8 bytes instead of a 64-byte bucket.
 struct WideDir {
   uint32_t node;
   uint32_t log2nb;      // log2 of the bucket count (>= 1)
@@ -112,7 +113,7 @@ struct WideDir {
   uint32_t flags;       // kWideFiltered
 };
 constexpr uint32_t kWideFiltered = 1u;
-constexpr uint32_t kFpMaxLog2 = 12;
+constexpr uint32_t kFpMaxLog2 = 16;
 constexpr uint32_t kBucketSlots = 8;
 struct WideBucket {
   uint32_t tok[kBucketSlots];

@@ -1763,7 +1763,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         }
         __syncthreads();
         const uint32_t m = min((uint32_t)kRankChunk, nS - ib);
-        if (j < nS) cntless += count_before<4>(rk_key, rk_node, m, myk, myn);
+        if (j < nS) cntless += count_before<8>(rk_key, rk_node, m, myk, myn);
       }
       if (j < nS && cntless < F) {
         onorm[cntless] = me.s * lnf[me.depth];

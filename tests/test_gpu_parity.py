@@ -243,8 +243,8 @@ def test_beam_1000(ft, po):
 
 
 @pytest.mark.parametrize("scan_mult,wide_min,fp_max", [
-    ("0", "0", "12"), ("0", "2", "12"), ("0", "2", "0"), ("999999", "512", "12"),
-    ("1", "64", "12"), ("1", "64", "0")])
+    ("0", "0", "16"), ("0", "2", "16"), ("0", "2", "0"), ("999999", "512", "16"),
+    ("1", "64", "16"), ("1", "64", "0")])
 def test_lookup_modes(ft, po, monkeypatch, scan_mult, wide_min, fp_max):
     # scan_mult 0 sends every parent with children to the binary search
     # (wide_min 0) or the hash tables (wide_min 2); 999999 scans all.
