@@ -90,7 +90,7 @@ struct ft_ctx {
   uint32_t scan_mult = 2;
   uint32_t wgs_req = 4096;    // workgroups per request (clamped to residency:
                               // a lone request gets every CU)
-  uint32_t share_min = 8192;  // work items from which a step is shared
+  uint32_t share_min = 4096;  // work items from which a step is shared
   int max_resident = 0;
   // ring of (start, end) event pairs, one pair per launch
   static constexpr size_t kRing = 1024;
