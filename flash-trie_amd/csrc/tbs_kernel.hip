@@ -1222,11 +1222,33 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   uint32_t n_cur = 1, nS = 0, hist_used = 0;
   uint64_t n_cands = 0;
   // the parent table of the step was written by the previous step's emit,
-  // and its row loaded into registers there (pf_*)
-  bool par_ready = false, row_pf = false;
+  // and its row loaded into registers there (pf_*); for step 0 both are
+  // read here, the root's entry by one thread of wave 1 while every thread
+  // reads its share of row 0
+  bool par_ready = true, row_pf = K <= (uint32_t)kBlock;
   uint32_t pf_id = 0;
   float pf_lp = 0.0f;
+  if (row_pf && tid < K) {
+    pf_id = rid[tid];
+    pf_lp = rlp[tid];
+  }
+  uint32_t root_err = 0;
+  if (tid == 64u) {
+    const ParEntry e = parent_entry(a, 0u, 0u, K, &root_err);
+    st_dev(&par_c0[0], e.c0);
+    st_dev(&par_aux[0], e.aux);
+    st_dev(&par_node[0], 0u);
+    st_dev(&par_mode[0], e.mode);
+    sm.p_c0[0] = e.c0;
+    sm.p_aux[0] = e.aux;
+    sm.p_node[0] = 0u;
+    sm.p_mode[0] = (uint8_t)e.mode;
+    sm.p_lp[0] = e.lp;
+    sm.p_s[0] = 0.0;
+    sm.p_hist[0] = kNoHist;
+  }
   __syncthreads();
+  if (root_err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
 
   for (uint32_t t = 0; t < T; ++t) {
     if (n_cur == 0 || (early && nS >= F)) break;
