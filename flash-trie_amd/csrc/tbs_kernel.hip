@@ -133,33 +133,40 @@ constexpr int kRankChunk = 1024;
 static_assert(offsetof(Smem, row_id) % 16 == 0 && offsetof(Smem, row_lp) % 16 == 0,
               "rank scratch is read 16 bytes at a time");
 static_assert(kRankChunk == kBlock, "a thread's own rank entry sits in its own chunk");
+static_assert(kRankChunk % 16 == 0, "rank chunks hold whole count_before rounds");
 
 // How many of the m LDS entries (rk_key[q], rk_node[q]) order before (k, n)
 // by (key, node).  Every thread reads the same entries (broadcast reads),
-// 2 * P keys per iteration through P 16-byte loads so the reads overlap; a
-// node is read only for an equal key.
+// 2 * P keys and their nodes per iteration through 3 * P / 2 16-byte loads
+// issued together, compared without branches (a branch per equal key made
+// every wave wait for all its outstanding reads).
 template <int P>
 __device__ __forceinline__ uint32_t count_before(const uint64_t* rk_key,
                                                  const uint32_t* rk_node, uint32_t m,
                                                  uint64_t k, uint32_t n) {
-  uint32_t c = 0, q = 0;
-  for (; q + 2 * P <= m; q += 2 * P) {
+  // m is a multiple of 2 * P; entries past the real ones are kRankPad keys
+  uint32_t c = 0;
+  for (uint32_t q = 0; q < m; q += 2 * P) {
     ulonglong2 v[P];
+    uint4 nd[P / 2];
 #pragma unroll
     for (int u = 0; u < P; ++u) v[u] = *(const ulonglong2*)&rk_key[q + 2 * u];
 #pragma unroll
-    for (int u = 0; u < P; ++u) {
-      c += (v[u].x < k) + (v[u].y < k);
-      if (v[u].x == k) c += rk_node[q + 2 * u] < n;
-      if (v[u].y == k) c += rk_node[q + 2 * u + 1] < n;
+    for (int u = 0; u < P / 2; ++u) nd[u] = *(const uint4*)&rk_node[q + 4 * u];
+#pragma unroll
+    for (int u = 0; u < P / 2; ++u) {
+      const ulonglong2 a = v[2 * u], b = v[2 * u + 1];
+      c += (a.x < k) | ((a.x == k) & (nd[u].x < n));
+      c += (a.y < k) | ((a.y == k) & (nd[u].y < n));
+      c += (b.x < k) | ((b.x == k) & (nd[u].z < n));
+      c += (b.y < k) | ((b.y == k) & (nd[u].w < n));
     }
-  }
-  for (; q < m; ++q) {
-    const uint64_t kk = rk_key[q];
-    c += (kk < k) || (kk == k && rk_node[q] < n);
   }
   return c;
 }
+// rank-scratch filler past the real entries: orders after every real key
+// (norm_key of a finite score is below it) and never counts
+constexpr uint64_t kRankPad = ~0ull;
 
 // lookup mode word of a parent: the mode, and whether the parent sits at
 // string depth t (only then can a child -- one token long, terminal --
@@ -1477,10 +1484,13 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             // in the thread's own chunk, entry i is its own
             rk_key[tid] = ib == jb ? myk : norm_key(cur[i].s * lnf_cur);
             rk_node[tid] = ib == jb ? myn : cur[i].node;
+          } else if (tid < (uint32_t)kRankChunk) {
+            rk_key[tid] = kRankPad;
+            rk_node[tid] = 0;
           }
           __syncthreads();
-          const uint32_t m = min((uint32_t)kRankChunk, ncur_now - ib);
-          if (j < ncur_now) cntless += count_before<4>(rk_key, rk_node, m, myk, myn);
+          const uint32_t m = (min((uint32_t)kRankChunk, ncur_now - ib) + 3u) & ~3u;
+          if (j < ncur_now) cntless += count_before<2>(rk_key, rk_node, m, myk, myn);
           __syncthreads();
         }
         if (j < ncur_now) rank[j] = cntless;
@@ -1782,9 +1792,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
             rk_key[tid] = norm_key(o.s * lnf[o.depth]);
             rk_node[tid] = o.node;
           }
+        } else if (tid < (uint32_t)kRankChunk) {
+          rk_key[tid] = kRankPad;
+          rk_node[tid] = 0;
         }
         __syncthreads();
-        const uint32_t m = min((uint32_t)kRankChunk, nS - ib);
+        const uint32_t m = (min((uint32_t)kRankChunk, nS - ib) + 15u) & ~15u;
         if (j < nS) cntless += count_before<8>(rk_key, rk_node, m, myk, myn);
       }
       if (j < nS && cntless < F) {
