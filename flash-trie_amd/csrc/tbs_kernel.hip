@@ -483,20 +483,53 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
       sm.collected = collect ? 1u : 0u;
     }
     __syncthreads();
-    visit_keys<6>(n, gk, [&](uint32_t i, bool ok, uint64_t k) {
-      const uint64_t hk = (k - base) & hi_mask;
-      const bool act = ok && hk == prefix;
-      const uint32_t o = wave_append(act, &sm.n_out);
-      if (act && o < (uint32_t)kBinCap) {
-        sm.bin_key[o] = k;
-        sm.bin_idx[o] = i;
+    // U keys per thread per round, all read before the first wait; each
+    // list gets one LDS append per wave per round (slots in the order
+    // (key slot u, lane))
+    constexpr uint32_t U = 6;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (uint32_t b0 = 0; b0 < n; b0 += U * kBlock) {
+      uint64_t k[U];
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) k[u] = gk(min(b0 + u * kBlock + tid, n - 1u));
+      uint32_t fa = 0, fb = 0, ca = 0, cb = 0;
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) {
+        const bool ok = b0 + u * kBlock + tid < n;
+        const uint64_t hk = (k[u] - base) & hi_mask;
+        const bool act = ok && hk == prefix;
+        const bool below = collect && ok && hk < prefix;
+        fa |= (uint32_t)act << u;
+        fb |= (uint32_t)below << u;
+        ca += (uint32_t)__popcll(__ballot(act));
+        cb += (uint32_t)__popcll(__ballot(below));
       }
-      if (collect) {
-        const bool below = ok && hk < prefix;
-        const uint32_t q = wave_append(below, &sm.n_keep);
-        if (below && q < (uint32_t)kKeepCap) sm.keep_idx[q] = i;
+      uint32_t ba = 0, bb = 0;
+      if (lane == 0) {
+        if (ca) ba = atomicAdd(&sm.n_out, ca);
+        if (cb) bb = atomicAdd(&sm.n_keep, cb);
       }
-    });
+      ba = (uint32_t)__builtin_amdgcn_readfirstlane((int)ba);
+      bb = (uint32_t)__builtin_amdgcn_readfirstlane((int)bb);
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t i = b0 + u * kBlock + tid;
+        const uint64_t ma = __ballot((fa >> u) & 1u), mb = __ballot((fb >> u) & 1u);
+        if ((fa >> u) & 1u) {
+          const uint32_t o = ba + (uint32_t)__popcll(ma & lt);
+          if (o < (uint32_t)kBinCap) {
+            sm.bin_key[o] = k[u];
+            sm.bin_idx[o] = i;
+          }
+        }
+        if ((fb >> u) & 1u) {
+          const uint32_t q = bb + (uint32_t)__popcll(mb & lt);
+          if (q < (uint32_t)kKeepCap) sm.keep_idx[q] = i;
+        }
+        ba += (uint32_t)__popcll(ma);
+        bb += (uint32_t)__popcll(mb);
+      }
+    }
     __syncthreads();
   }
   // cnt keys in LDS share the prefix above `top`: 8-bit digits downwards,
