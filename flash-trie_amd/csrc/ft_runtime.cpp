@@ -74,7 +74,7 @@ struct ft_ctx {
   uint64_t per_req = 0;   // staging bytes bound of one request
 
   // wide-node index (device)
-  WideDir* d_wdir = nullptr;
+  WideDirGroup* d_wdir = nullptr;
   WideBucket* d_wtab = nullptr;
   uint64_t* d_wfp = nullptr;     // per bucket: slot fingerprints
   uint32_t* d_labels = nullptr;  // per node: first token | kSlotSel
@@ -323,23 +323,38 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   for (auto& e : ent) e.flags = e.log2nb <= fp_max ? kWideFiltered : 0u;
   uint64_t n_ok = 0;
   for (size_t i = 0; i < ent.size(); ++i) n_ok += failed[i] ? 0 : 1;
-  uint32_t dlg = 1;
-  while ((1ull << dlg) < 2 * std::max<uint64_t>(n_ok, 1)) ++dlg;
-  std::vector<WideDir> dir(1ull << dlg, WideDir{kEmpty, 0, 0, 0});
+  // directory groups, load <= 1/2
+  uint32_t dlg = 0;
+  while (((uint64_t)kDirSlots << dlg) < 2 * std::max<uint64_t>(n_ok, 1)) ++dlg;
+  WideDirGroup empty_group;
+  for (uint32_t k = 0; k < kDirSlots; ++k) {
+    empty_group.node[k] = kEmpty;
+    empty_group.bucket_off[k] = empty_group.lgf[k] = empty_group.pad[k] = 0;
+  }
+  std::vector<WideDirGroup> dir(1ull << dlg, empty_group);
   for (size_t i = 0; i < ent.size(); ++i) {
     if (failed[i]) continue;  // searched by binary search instead
-    uint32_t sl = fib_slot(ent[i].node, dlg);
-    while (dir[sl].node != kEmpty) sl = (sl + 1) & ((1u << dlg) - 1);
-    dir[sl] = ent[i];
+    uint32_t g = fib_slot(ent[i].node, dlg);
+    for (;;) {
+      uint32_t k = 0;
+      while (k < kDirSlots && dir[g].node[k] != kEmpty) ++k;
+      if (k < kDirSlots) {
+        dir[g].node[k] = ent[i].node;
+        dir[g].bucket_off[k] = ent[i].bucket_off;
+        dir[g].lgf[k] = ent[i].log2nb | (ent[i].flags << 8);
+        break;
+      }
+      g = (g + 1) & ((1u << dlg) - 1);
+    }
   }
   hipError_t e;
-  if ((e = hipMalloc(&c->d_wdir, dir.size() * sizeof(WideDir))) != hipSuccess)
+  if ((e = hipMalloc(&c->d_wdir, dir.size() * sizeof(WideDirGroup))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide dir)");
   if ((e = hipMalloc(&c->d_wtab, buckets * sizeof(WideBucket))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide tables)");
   if ((e = hipMalloc(&c->d_wfp, buckets * sizeof(uint64_t))) != hipSuccess)
     return hip_fail(e, "hipMalloc(wide fingerprints)");
-  if ((e = hipMemcpy(c->d_wdir, dir.data(), dir.size() * sizeof(WideDir),
+  if ((e = hipMemcpy(c->d_wdir, dir.data(), dir.size() * sizeof(WideDirGroup),
                      hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(e, "hipMemcpy(wide dir)");
   if ((e = hipMemcpy(c->d_wtab, tab.get(), buckets * sizeof(WideBucket),

@@ -95,8 +95,11 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 // word kSlotEmptyTok, which no stored token equals (a node with a child
 // token >= kSlotEmptyTok gets no table), so a lookup can match token words
 // alone and read the child word of the matching slot only.  Tables are
-// found through a directory keyed by node id (Fibonacci hashing, linear
-// probing, node 0xFFFFFFFF marks an empty entry).
+// found through a directory keyed by node id: 2^wdir_log2 groups of
+// kDirSlots entries, one 64-byte line each; an entry sits in the first free
+// slot of its home group fib_slot(node) or, when that is full, of the next
+// groups in turn (load <= 1/2), so a lookup reads whole groups and stops at
+// the first group with a free slot -- almost always after one read.
 //
 // Every bucket also has an 8-byte fingerprint word: byte s is
 // wide_fp(token) of slot s, 0 for an empty slot.  For a table of at most
@@ -106,12 +109,20 @@ __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
 // fingerprints are 1/8 of a table's bytes (those of a small table stay
 // cached across the K lookups of a step), and most lookups are misses that
 // then read 8 bytes instead of a 64-byte bucket.
-struct WideDir {
+struct WideDir {        // one node's table (host side)
   uint32_t node;
   uint32_t log2nb;      // log2 of the bucket count (>= 1)
   uint32_t bucket_off;  // first bucket of the node's table
   uint32_t flags;       // kWideFiltered
 };
+constexpr uint32_t kDirSlots = 4;
+struct WideDirGroup {   // kDirSlots directory entries (device side)
+  uint32_t node[kDirSlots];        // kEmpty: a free slot
+  uint32_t bucket_off[kDirSlots];
+  uint32_t lgf[kDirSlots];         // log2nb | flags << 8
+  uint32_t pad[kDirSlots];
+};
+static_assert(sizeof(WideDirGroup) == 64, "WideDirGroup layout");
 constexpr uint32_t kWideFiltered = 1u;
 constexpr uint32_t kFpMaxLog2 = 16;
 constexpr uint32_t kBucketSlots = 8;
@@ -180,7 +191,7 @@ struct KArgs {
   WsLayout lay;
   uint32_t batch;
   uint32_t scan_limit;
-  const WideDir* wdir;   // null: no wide-node index
+  const WideDirGroup* wdir;  // null: no wide-node index
   const WideBucket* wtab;
   const uint64_t* wfp;   // fingerprint word per bucket
   const uint32_t* labels;  // per node: first token | kSlotSel

@@ -686,19 +686,29 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
     e.mode = M_SEARCH;
     e.work = K;
     if (a.wdir && deg >= a.wide_min) {
-      // this node has a table: find it in the directory
+      // this node has a table: find it in the directory, a 64-B group of
+      // entries per read from the home group on
       const uint32_t mask = (1u << a.wdir_log2) - 1u;
-      uint32_t sl = fib_slot(node, a.wdir_log2);
+      uint32_t g = fib_slot(node, a.wdir_log2);
       for (uint32_t it = 0; it <= mask; ++it) {
-        const WideDir w = a.wdir[sl];
-        if (w.node == node) {
-          e.mode = M_HASH | ((w.flags & kWideFiltered) ? kModeFiltered : 0u);
-          e.aux = w.log2nb;
-          e.c0 = w.bucket_off;
-          break;
+        const uint4* gp = (const uint4*)&a.wdir[g];
+        const uint4 nd = gp[0], off = gp[1], lgf = gp[2];
+        const uint32_t nds[4] = {nd.x, nd.y, nd.z, nd.w};
+        const uint32_t offs[4] = {off.x, off.y, off.z, off.w};
+        const uint32_t lgfs[4] = {lgf.x, lgf.y, lgf.z, lgf.w};
+        bool found = false, has_free = false;
+#pragma unroll
+        for (int k = 0; k < (int)kDirSlots; ++k) {
+          if (nds[k] == node) {
+            found = true;
+            e.mode = M_HASH | (((lgfs[k] >> 8) & kWideFiltered) ? kModeFiltered : 0u);
+            e.aux = lgfs[k] & 0xFFu;
+            e.c0 = offs[k];
+          }
+          has_free = has_free || nds[k] == kEmpty;
         }
-        if (w.node == kEmpty) break;
-        sl = (sl + 1) & mask;
+        if (found || has_free) break;
+        g = (g + 1) & mask;
       }
     }
   }
