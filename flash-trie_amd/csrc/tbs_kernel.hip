@@ -851,38 +851,20 @@ struct StepView {
 // nwaves waves, so every wave gets an even share of every region of the
 // item space (hashed parents cost a random read per item, scanned ones a
 // coalesced one).  This workgroup's waves are gwave0 .. gwave0 + kWaves - 1.
-// With at most kBlock parents the parent table is read from LDS: the leader
-// has written it there (`par_in_lds`), a helper copies it in first.  Pushes
-// go to the request's global buffers.  A `solo` workgroup expands the whole
+// With at most kBlock parents the parent table is read from LDS, where the
+// caller has put it (the leader in its parent phase, a helper with the row);
+// the caller has also zeroed this workgroup's push counters and
+// synchronised.  The `leader` also reads, for its own emit, the next pending
+// token of each link parent that stays one.  Pushes go to the request's
+// global buffers.  A `solo` workgroup expands the whole
 // step alone: its LDS counters are the list lengths and the control block is
 // not used (the counts stay in sm.lq_next, sm.lq_sel, sm.w_children and
 // sm.w_probes).
 __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, uint32_t W,
-                             uint32_t gwave0, uint32_t nwaves, bool par_in_lds,
-                             bool solo, bool hashed, Smem& sm) {
+                             uint32_t gwave0, uint32_t nwaves, bool leader, bool solo,
+                             bool hashed, Smem& sm) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const bool lds_par = v.n_par <= (uint32_t)kBlock;
-  if (!par_in_lds) {
-    if (lds_par) {
-      for (uint32_t i = tid; i <= v.n_par; i += kBlock) sm.woff[i] = ld_relaxed(&v.woff[i]);
-      for (uint32_t i = tid; i < v.n_par; i += kBlock) {
-        sm.p_c0[i] = ld_relaxed(&v.pc0[i]);
-        sm.p_aux[i] = ld_relaxed(&v.paux[i]);
-        sm.p_node[i] = ld_relaxed(&v.pnode[i]);
-        sm.p_mode[i] = (uint8_t)ld_relaxed(&v.pmode[i]);
-        const CurRec p = ld_cur(&v.cur[i]);
-        sm.p_s[i] = p.s;
-        sm.p_hist[i] = p.hist;
-      }
-    }
-    if (tid == 0) {
-      sm.w_children = 0;
-      sm.w_probes = 0;
-      sm.lq_next = 0;
-      sm.lq_sel = 0;
-    }
-    __syncthreads();
-  }
   uint32_t my_children = 0, my_probes = 0;
   const uint32_t K = v.K, t = v.t;
   const uint32_t nchunks = (W + 63u) >> 6;
@@ -925,7 +907,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
         // the leader reads the next pending token of a link parent that
         // stays one (for its emit) while the row is searched
         uint32_t xtok = kNoToken;
-        if (par_in_lds && lds_par && md == M_LP_NEXT) {
+        if (leader && lds_par && md == M_LP_NEXT) {
           const uint32_t tc = sm.p_lp[pj];
           if (tc != kNoCursor) xtok = a.tail[tc + 1u];
         }
@@ -1104,26 +1086,33 @@ __device__ __forceinline__ void load_row(const uint32_t* rid, const float* rlp, 
   }
 }
 
-// Hashes the LDS row (K <= kRowHashMaxK; the workgroup has synchronised since
-// load_row).  Tokens >= 2^31 - 1 never match a trie token and are left out.
-// Row tokens are distinct (staging rejects duplicates) and fill at most half
-// the table, so every insert ends in a free slot.  Ends synchronised.
-__device__ __forceinline__ void hash_row(uint32_t K, Smem& sm) {
+// The row hash: emptied by every thread's share of the slots, then filled
+// with (token, sorted position) pairs.  Tokens >= 2^31 - 1 never match a trie
+// token and are left out.  Row tokens are distinct (staging rejects
+// duplicates) and fill at most half the table (K <= kRowHashMaxK), so every
+// insert ends in a free slot.
+__device__ __forceinline__ void row_hash_clear(Smem& sm) {
   for (uint32_t i = threadIdx.x; i < (uint32_t)kRowHash; i += kBlock)
     sm.rh_tok[i] = kRowHashEmpty;
-  __syncthreads();
-  for (uint32_t p = threadIdx.x; p < K; p += kBlock) {
-    const uint32_t tok = sm.row_id[p];
-    if (tok >= kTokMask) continue;
-    uint32_t h = row_hash(tok);
-    for (int it = 0; it < kRowHash; ++it) {
-      if (atomicCAS(&sm.rh_tok[h], kRowHashEmpty, tok) == kRowHashEmpty) {
-        sm.rh_pos[h] = (uint16_t)p;
-        break;
-      }
-      h = (h + 1) & (kRowHash - 1);
+}
+__device__ __forceinline__ void row_hash_insert(uint32_t tok, uint32_t p, Smem& sm) {
+  if (tok >= kTokMask) return;
+  uint32_t h = row_hash(tok);
+  for (int it = 0; it < kRowHash; ++it) {
+    if (atomicCAS(&sm.rh_tok[h], kRowHashEmpty, tok) == kRowHashEmpty) {
+      sm.rh_pos[h] = (uint16_t)p;
+      return;
     }
+    h = (h + 1) & (kRowHash - 1);
   }
+}
+
+// Hashes the LDS row (the workgroup has synchronised since the row was
+// written).  Ends synchronised.
+__device__ __forceinline__ void hash_row(uint32_t K, Smem& sm) {
+  row_hash_clear(sm);
+  __syncthreads();
+  for (uint32_t p = threadIdx.x; p < K; p += kBlock) row_hash_insert(sm.row_id[p], p, sm);
   __syncthreads();
 }
 
@@ -1139,6 +1128,7 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
   const double* lnf = (const double*)in;
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
   const float* rlp = (const float*)(in + d.rlp_off);
+  row_hash_clear(sm);  // (visible after the first barrier below)
   for (;;) {
     if (tid == 0) {
       unsigned long long v = 0;
@@ -1193,12 +1183,48 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.sent_thr = d.sent_thr;
     sv.keep_lds_max = 0;
     sv.one_each = false;
-    load_row(rid, rlp, t, d.K, sm);
-    __syncthreads();
+    // the step's row (into the row hash too: emptied after the previous
+    // step) and parent table in one round of reads
     const bool hashed = d.K <= kRowHashMaxK;
-    if (hashed) hash_row(d.K, sm);
+    const bool lds_par = n_par <= (uint32_t)kBlock;
+    const uint64_t ro = (uint64_t)t * d.K;
+    const uint32_t nload = max(d.K, lds_par ? n_par + 1u : 0u);
+    for (uint32_t i = tid; i < nload; i += kBlock) {
+      uint32_t tok = 0;
+      float lp = 0.0f;
+      if (i < d.K) {
+        tok = rid[ro + i];
+        lp = rlp[ro + i];
+      }
+      if (lds_par && i <= n_par) {
+        sm.woff[i] = ld_relaxed(&sv.woff[i]);
+        if (i < n_par) {
+          sm.p_c0[i] = ld_relaxed(&sv.pc0[i]);
+          sm.p_aux[i] = ld_relaxed(&sv.paux[i]);
+          sm.p_node[i] = ld_relaxed(&sv.pnode[i]);
+          sm.p_mode[i] = (uint8_t)ld_relaxed(&sv.pmode[i]);
+          const CurRec p = ld_cur(&sv.cur[i]);
+          sm.p_s[i] = p.s;
+          sm.p_hist[i] = p.hist;
+        }
+      }
+      if (i < d.K) {
+        sm.row_id[i] = tok;
+        sm.row_lp[i] = lp;
+        if (hashed) row_hash_insert(tok, i, sm);
+      }
+    }
+    if (tid == 0) {
+      sm.w_children = 0;
+      sm.w_probes = 0;
+      sm.lq_next = 0;
+      sm.lq_sel = 0;
+    }
+    __syncthreads();
     expand_range(a, sv, W, g * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, false, false,
                  hashed, sm);
+    // the row lookups are done: empty the hash for the next step
+    if (hashed) row_hash_clear(sm);
     wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
     if (tid == 0) atomicAdd(&ctl->done, 1u);
