@@ -162,8 +162,9 @@ def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py measures one GPU: the search shards by request "
-              "(replicated trie) with no exchange, see DESIGN.md; "
-              f"--gpus {args.gpus} is not run here", file=sys.stderr)
+              "(a replicated trie, no exchange between GPUs), so the "
+              f"aggregate is the per-GPU rate times the GPU count; --gpus "
+              f"{args.gpus} is not run here", file=sys.stderr)
         sys.exit(2)
     import build as ftbuild
     if not ftbuild.built():
