@@ -1233,7 +1233,9 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
 
 __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   __shared__ Smem sm;
-  // request-major interleave: request r owns blocks r, r + batch, ...
+  // request-major interleave: request r owns blocks r, r + batch, ...  The
+  // dispatcher deals blocks to the 8 XCDs round-robin, so at batch 8 each
+  // request's workgroups share one XCD and its L2.
   const uint32_t req = blockIdx.x % a.batch;
   const uint32_t g = blockIdx.x / a.batch;
   const uint32_t tid = threadIdx.x;
