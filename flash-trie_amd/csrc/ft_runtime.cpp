@@ -45,6 +45,8 @@ struct StagedReq {
   uint32_t T = 0, K = 0, F = 0;
   bool skip = false;
   uint64_t out_bytes = 0;
+  uint64_t bmax = 0;  // widest beam of any step (and the final beam)
+  uint64_t hsum = 0;  // sum of the beam widths: bounds the history records
 };
 
 }  // namespace
@@ -82,8 +84,16 @@ struct ft_ctx {
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
 
   std::vector<StagedReq> staged;
+  std::vector<std::pair<uint32_t, uint32_t>> sort_tmp;  // max_topk pairs
+  // staged requests launched since the last ft_stage (ft_fetch reports the
+  // others as FT_E_STATE instead of returning whatever d_out holds)
+  std::vector<uint8_t> launched_slot;
   uint64_t out_stride = 0;
   bool launched = false;
+  // recorded after each staging copy: the next ft_stage waits for it before
+  // it rewrites the pinned buffer that copy reads
+  hipEvent_t stage_ev = nullptr;
+  bool stage_pending = false;
   // parents with at most scan_mult * K children are scanned (one work item
   // per child), wider ones use their hash table (K items): scanning a child
   // is a coalesced 4-B read, a hashed proposal a random 64-B bucket
@@ -185,6 +195,90 @@ static void cuckoo_settle(WideBucket* tb, uint32_t lg) {
           }
       }
   }
+}
+
+// Checks every structural fact the kernel relies on before any of the image
+// reaches the device, so that a corrupt or hand-made blob is an FT_E_IMAGE
+// and never an out-of-bounds read on the GPU:
+//  * BFS child ranges: rec[0] starts the root's children at id 1, ranges are
+//    non-decreasing and end at the sentinel rec[N].child_begin == N, and a
+//    node's children have larger ids than the node (so parent walks end);
+//  * every child c of v has parent[c] == v, an edge of >= 1 token with
+//    string depth depth(v) + edge length (a link node exactly when the edge
+//    has >= 2 tokens), siblings in strictly ascending first-token order and
+//    tokens below 2^31 - 1;
+//  * a link node's edge lies inside tail[] and starts with its first token;
+//  * the terminal flags count num_keys.
+// Parent ranges are split over host threads (each child is checked by the
+// thread that owns its parent).
+static int validate_image_host(const uint8_t* image, const ft_image_header& h) {
+  const uint64_t N = h.num_nodes;
+  const ft_node_rec* R = (const ft_node_rec*)(image + h.recs_offset);
+  const uint32_t* P = (const uint32_t*)(image + h.parent_offset);
+  const uint32_t* Tl = (const uint32_t*)(image + h.tail_offset);
+  if (h.parent_offset % 4 || h.tail_offset % 4)
+    return fail(FT_E_IMAGE, "ft_create: misaligned parent or tail array");
+  if (R[0].child_begin != 1)
+    return fail(FT_E_IMAGE, "ft_create: the root's children must start at id 1");
+  if (R[N].child_begin != N)
+    return fail(FT_E_IMAGE, "ft_create: sentinel child_begin must equal num_nodes");
+  if ((R[0].meta & (FT_META_DEPTH_MASK | FT_META_LINK)) != 0)
+    return fail(FT_E_IMAGE, "ft_create: the root must have depth 0 and no edge");
+  const int T = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<uint64_t> keys(T, 0);
+  // first bad node per thread (N: none) and what was wrong with it
+  std::vector<uint64_t> bad(T, N);
+  std::vector<int> why(T, 0);
+  {
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&, w]() {
+        const uint64_t b = N * w / T, e = N * (w + 1) / T;
+        uint64_t k = 0;
+        for (uint64_t v = b; v < e; ++v) {
+          const uint32_t c0 = R[v].child_begin, c1 = R[v + 1].child_begin;
+          if (c1 < c0 || c1 > N || (c1 > c0 && c0 <= v)) {
+            bad[w] = v, why[w] = 1;
+            return;
+          }
+          if (R[v].meta & FT_META_TERMINAL) ++k;
+          const uint32_t sd = R[v].meta & FT_META_DEPTH_MASK;
+          for (uint32_t c = c0; c < c1; ++c) {
+            const uint32_t m = R[c].meta;
+            const uint32_t el = (m >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+            if (P[c] != v || el == 0 || (m & FT_META_DEPTH_MASK) != sd + el ||
+                ((m & FT_META_LINK) != 0) != (el >= 2) ||
+                (c > c0 && R[c].first_tok <= R[c - 1].first_tok) ||
+                R[c].first_tok >= kSlotEmptyTok) {
+              bad[w] = c, why[w] = 2;
+              return;
+            }
+            if ((m & FT_META_LINK) &&
+                ((uint64_t)R[c].tail_off + el > h.tail_len ||
+                 Tl[R[c].tail_off] != R[c].first_tok)) {
+              bad[w] = c, why[w] = 3;
+              return;
+            }
+          }
+        }
+        keys[w] = k;
+      });
+    for (auto& x : th) x.join();
+  }
+  static const char* const kWhy[] = {"", "child range is not breadth first",
+                                     "is inconsistent with its parent (parent, edge, "
+                                     "depth, sibling order or token id >= 2^31 - 1)",
+                                     "has an edge outside tail[]"};
+  uint64_t nkeys = 0;
+  for (int w = 0; w < T; ++w) {
+    if (bad[w] != N)
+      return fail(FT_E_IMAGE, "ft_create: node " + std::to_string(bad[w]) + " " +
+                                  kWhy[why[w]]);
+    nkeys += keys[w];
+  }
+  if (nkeys != h.num_keys)
+    return fail(FT_E_IMAGE, "ft_create: num_keys does not match the terminal flags");
+  return FT_OK;
 }
 
 // Per node, its first edge token with kSlotSel when the node can close a
@@ -406,6 +500,8 @@ int ft_create(const void* image, size_t image_bytes, int device,
       h.parent_offset + h.num_nodes * 4 > image_bytes ||
       h.tail_offset + h.tail_len * 4 > image_bytes || h.recs_offset % 16)
     return fail(FT_E_IMAGE, "ft_create: inconsistent image header");
+  // the whole image is checked before any device call
+  if (int rc = validate_image_host((const uint8_t*)image, h)) return rc;
 
   int ndev = 0;
   hipError_t e = hipGetDeviceCount(&ndev);
@@ -448,6 +544,7 @@ int ft_create(const void* image, size_t image_bytes, int device,
   }
   c->ring.assign(2 * ft_ctx::kRing, nullptr);
   for (auto& ev : c->ring) (void)hipEventCreate(&ev);
+  (void)hipEventCreateWithFlags(&c->stage_ev, hipEventDisableTiming);
   if (int rc = build_labels(c, (const uint8_t*)image)) {
     ft_destroy(c);
     return rc;
@@ -483,6 +580,35 @@ int ft_create(const void* image, size_t image_bytes, int device,
 // stale control word must never look like a step posted by this launch.
 static std::atomic<uint32_t> g_launch_epoch{0};
 
+// Byte layout of one request's workspace slot for beams of at most B
+// hypotheses, rows of at most K proposals and `hist` history records; the
+// candidate lists are sized so that no push can overflow (B * K pushes into
+// `next`, B * K + B into `selected`).  Returns the slot stride.
+static uint64_t ws_layout(uint64_t B, uint64_t K, uint64_t hist, WsLayout* out) {
+  const uint64_t BK = B * K;
+  WsLayout L{};
+  uint64_t off = 0;
+  L.cur0 = off; off = align_up(off + B * sizeof(CurRec), 256);
+  L.cur1 = off; off = align_up(off + B * sizeof(CurRec), 256);
+  L.nextc = off; off = align_up(off + BK * sizeof(NextRec), 256);
+  L.selA = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
+  L.selB = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
+  L.rank = off; off = align_up(off + B * 4, 256);
+  L.hist = off; off = align_up(off + hist * sizeof(HistRec), 256);
+  L.ctl = off; off = align_up(off + sizeof(Ctl), 256);
+  L.par_c0 = off; off = align_up(off + B * 4, 256);
+  L.par_aux = off; off = align_up(off + B * 4, 256);
+  L.par_node = off; off = align_up(off + B * 4, 256);
+  L.par_mode = off; off = align_up(off + B * 4, 256);
+  L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
+  L.next_cap = (uint32_t)BK;
+  L.sel_cap = (uint32_t)(BK + B);
+  L.hist_cap = (uint32_t)hist;
+  L.cur_cap = (uint32_t)B;
+  *out = L;
+  return off;
+}
+
 int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
                size_t max_out_beams, size_t max_out_tokens,
                size_t max_inter_beams) {
@@ -501,31 +627,13 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   if (max_inter_beams >= 0xFFFFFFF0ull)
     return fail(FT_E_LIMIT, "ft_reserve: max_num_inter_beams too large");
   (void)hipSetDevice(c->device);
+  // nothing queued may still read or write the buffers freed here
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  c->stage_pending = false;
   release_workspace(c);
   const uint64_t B = max_out_beams, K = max_topk;
-  const uint64_t BK = B * K;
-  if (BK + B >= 0xFFFFFFF0ull) return fail(FT_E_LIMIT, "ft_reserve: beams * topk too large");
-  WsLayout L{};
-  uint64_t off = 0;
-  L.cur0 = off; off = align_up(off + B * sizeof(CurRec), 256);
-  L.cur1 = off; off = align_up(off + B * sizeof(CurRec), 256);
-  L.nextc = off; off = align_up(off + BK * sizeof(NextRec), 256);
-  L.selA = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
-  L.selB = off; off = align_up(off + (BK + B) * sizeof(SelRec), 256);
-  L.rank = off; off = align_up(off + B * 4, 256);
-  L.hist = off; off = align_up(off + (uint64_t)max_inter_beams * sizeof(HistRec), 256);
-  L.ctl = off; off = align_up(off + sizeof(Ctl), 256);
-  L.par_c0 = off; off = align_up(off + B * 4, 256);
-  L.par_aux = off; off = align_up(off + B * 4, 256);
-  L.par_node = off; off = align_up(off + B * 4, 256);
-  L.par_mode = off; off = align_up(off + B * 4, 256);
-  L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
-  L.next_cap = (uint32_t)BK;
-  L.sel_cap = (uint32_t)(BK + B);
-  L.hist_cap = (uint32_t)max_inter_beams;
-  L.cur_cap = (uint32_t)B;
-  c->lay = L;
-  c->ws_stride = off;
+  if (B * K + B >= 0xFFFFFFF0ull) return fail(FT_E_LIMIT, "ft_reserve: beams * topk too large");
+  c->ws_stride = ws_layout(B, K, max_inter_beams, &c->lay);
   c->out_slot_max = align_up(step_stats_offset((uint32_t)B, 0) + 4 * (uint64_t)max_out_tokens +
                                  8ull * kStepStats * max_steps + 8, 256);
   // per request: lnf + beams + sorted rows (token, logp, index) + key bounds
@@ -542,12 +650,14 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   if (rc) return release_workspace(c), rc;
   c->max_batch = max_batch;
   c->max_topk = max_topk;
+  c->sort_tmp.assign(max_topk, {0u, 0u});
   c->max_steps = max_steps;
   c->max_out_beams = max_out_beams;
   c->max_out_tokens = max_out_tokens;
   c->max_inter = max_inter_beams;
   c->reserved = true;
   c->staged.clear();
+  c->launched_slot.clear();
   c->launched = false;
   return FT_OK;
 }
@@ -561,26 +671,31 @@ static uint64_t host_norm_key(double v) {
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
-int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
-  if (!c || (!reqs && batch)) return fail(FT_E_ARG, "ft_stage: null argument");
-  if (!c->reserved) return fail(FT_E_STATE, "ft_stage: init_tbs_gpu (ft_reserve) was not called");
-  if (batch == 0 || batch > c->max_staged)
-    return fail(FT_E_LIMIT, "ft_stage: batch size " + std::to_string(batch) +
-                                " not in [1, " + std::to_string(c->max_staged) + "]");
-  c->staged.assign(batch, StagedReq());
-  c->launched = false;
-  uint8_t* H = c->h_stage;
+// Limits a staged request must respect (the reserved workspace, or the
+// no-allocation scratch).
+struct StageLimits {
+  uint64_t max_steps, max_topk, max_out_beams, max_out_tokens;
+};
+
+// Validates `batch` requests and packs them into H (cap bytes): DevReq[batch]
+// then each request's block (length-norm table, beam widths, token-sorted
+// rows, key bounds).  Fills staged[0, batch); *bytes = bytes used,
+// *out_stride = output bytes per request.  `tmp` holds max_topk pairs
+// (sorting an unsorted row).  Allocates nothing on success.
+static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& lim,
+                      uint8_t* H, uint64_t cap, StagedReq* staged,
+                      std::pair<uint32_t, uint32_t>* tmp, uint64_t* bytes,
+                      uint64_t* out_stride) {
   DevReq* D = (DevReq*)H;
   uint64_t off = align_up(batch * sizeof(DevReq), 256);
   uint64_t max_out = sizeof(OutHeader);
-  std::vector<std::pair<uint32_t, uint32_t>> tmp;
   for (size_t r = 0; r < batch; ++r) {
     const ft_request& q = reqs[r];
-    const std::string who = "request " + std::to_string(r) + ": ";
+    auto who = [r]() { return "request " + std::to_string(r) + ": "; };
     DevReq d{};
-    StagedReq& st = c->staged[r];
+    StagedReq& st = staged[r];
     if (q.num_beams == 0 || !q.beams)
-      return fail(FT_E_INPUT, who + "beams is empty");
+      return fail(FT_E_INPUT, who() + "beams is empty");
     const uint32_t F = q.beams[q.num_beams - 1];
     if (F == 0) {  // outputs untouched (louds-trie.cc:114-117)
       st.skip = true;
@@ -591,29 +706,36 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     }
     const uint32_t T = q.num_steps, K = q.topk;
     if (T == 0 || K == 0)
-      return fail(FT_E_INPUT, who + "topk rows are empty");
+      return fail(FT_E_INPUT, who() + "topk rows are empty");
     if (q.num_beams < T)
-      return fail(FT_E_INPUT, who + "fewer beam widths than topk rows");
-    if (T > c->max_steps)
-      return fail(FT_E_LIMIT, who + "steps " + std::to_string(T) +
-                                  " > max_num_outpos " + std::to_string(c->max_steps));
-    if (K > c->max_topk)
-      return fail(FT_E_LIMIT, who + "topk " + std::to_string(K) +
-                                  " > max_num_topk " + std::to_string(c->max_topk));
-    if (F > c->max_out_beams)
-      return fail(FT_E_LIMIT, who + "final beam > max_num_out_beams");
-    if ((uint64_t)F * T > c->max_out_tokens)
-      return fail(FT_E_LIMIT, who + "final beam * steps > max_num_out_tokens");
+      return fail(FT_E_INPUT, who() + "fewer beam widths than topk rows");
+    if (T > lim.max_steps)
+      return fail(FT_E_LIMIT, who() + "steps " + std::to_string(T) +
+                                  " > max_num_outpos " + std::to_string(lim.max_steps));
+    if (K > lim.max_topk)
+      return fail(FT_E_LIMIT, who() + "topk " + std::to_string(K) +
+                                  " > max_num_topk " + std::to_string(lim.max_topk));
+    if (F > lim.max_out_beams)
+      return fail(FT_E_LIMIT, who() + "final beam > max_num_out_beams");
+    if ((uint64_t)F * T > lim.max_out_tokens)
+      return fail(FT_E_LIMIT, who() + "final beam * steps > max_num_out_tokens");
     for (uint32_t t = 0; t < T; ++t) {
       if (q.beams[t] == 0)
-        return fail(FT_E_INPUT, who + "beam width 0 at step " + std::to_string(t));
-      if (q.beams[t] > c->max_out_beams)
-        return fail(FT_E_LIMIT, who + "beam width > max_num_out_beams");
+        return fail(FT_E_INPUT, who() + "beam width 0 at step " + std::to_string(t));
+      if (q.beams[t] > lim.max_out_beams)
+        return fail(FT_E_LIMIT, who() + "beam width > max_num_out_beams");
     }
     if (!q.topk_id_rows && (!q.topk_id || !q.topk_logp))
-      return fail(FT_E_ARG, who + "null topk arrays");
+      return fail(FT_E_ARG, who() + "null topk arrays");
     if (q.topk_id_rows && !q.topk_logp_rows)
-      return fail(FT_E_ARG, who + "null topk_logp rows");
+      return fail(FT_E_ARG, who() + "null topk_logp rows");
+    // the request's block must fit before anything is written
+    const uint64_t need = align_up(8ull * (T + 1), 16) + align_up(4ull * T, 16) +
+                          2 * align_up(4ull * T * K, 16) + align_up(2ull * T * K, 16) +
+                          align_up(16ull * T, 16);
+    if (off + need > cap)
+      return fail(FT_E_LIMIT, who() + "the staged batch exceeds the staging buffer (" +
+                                  std::to_string(cap) + " bytes)");
     d.T = T;
     d.K = K;
     d.F = F;
@@ -630,7 +752,7 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     for (uint32_t dd = 0; dd <= T; ++dd) {
       lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
       if (dd > 0 && !std::isfinite(lnf[dd]))
-        return fail(FT_E_INPUT, who + "length_norm gives a non-finite factor");
+        return fail(FT_E_INPUT, who() + "length_norm gives a non-finite factor");
     }
     o = align_up(o + 8ull * (T + 1), 16);
     d.beams_off = (uint32_t)o;
@@ -650,12 +772,12 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
     for (uint32_t t = 0; t < T; ++t) {
       const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
       const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
-      if (!rid || !rlp) return fail(FT_E_ARG, who + "null topk row");
+      if (!rid || !rlp) return fail(FT_E_ARG, who() + "null topk row");
       bool sorted = true;
       for (uint32_t k = 0; k < K; ++k) {
         const float x = rlp[k];
         if (std::isnan(x) || x == std::numeric_limits<float>::infinity())
-          return fail(FT_E_INPUT, who + "topk_logp holds NaN or +inf");
+          return fail(FT_E_INPUT, who() + "topk_logp holds NaN or +inf");
         if (k && rid[k] <= rid[k - 1]) sorted = false;
       }
       uint32_t* oid = rid_s + (uint64_t)t * K;
@@ -667,12 +789,11 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
         for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
         continue;
       }
-      tmp.resize(K);
       for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
-      std::sort(tmp.begin(), tmp.end());
+      std::sort(tmp, tmp + K);
       for (uint32_t p = 0; p < K; ++p) {
         if (p && tmp[p].first == tmp[p - 1].first)
-          return fail(FT_E_INPUT, who + "duplicate token id " +
+          return fail(FT_E_INPUT, who() + "duplicate token id " +
                                       std::to_string(tmp[p].first) +
                                       " in topk row " + std::to_string(t));
         oid[p] = tmp[p].first;
@@ -711,47 +832,80 @@ int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
       }
     }
     off = align_up(off + o, 256);
-    if (off > c->stage_cap) return fail(FT_E_LIMIT, "ft_stage: staging overflow");
+    if (off > cap) return fail(FT_E_LIMIT, "ft_stage: staging overflow");
     st.T = T;
     st.K = K;
     st.F = F;
+    {
+      uint64_t bmax = F, hsum = 0;
+      for (uint32_t t = 0; t < T; ++t) {
+        bmax = std::max<uint64_t>(bmax, q.beams[t]);
+        hsum += q.beams[t];
+      }
+      st.bmax = bmax;
+      st.hsum = hsum;
+    }
     st.out_bytes = step_stats_offset(F, T) + 8ull * kStepStats * T;
     max_out = std::max(max_out, st.out_bytes);
     D[r] = d;
   }
-  c->out_stride = align_up(max_out, 256);
-  (void)hipSetDevice(c->device);
-  hipError_t e = hipMemcpyAsync(c->d_stage, c->h_stage, off, hipMemcpyHostToDevice, c->stream);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(stage)");
+  *out_stride = align_up(max_out, 256);
+  *bytes = off;
   return FT_OK;
 }
 
-int ft_launch(ft_ctx* c) {
-  if (!c) return fail(FT_E_ARG, "ft_launch: null context");
-  return ft_launch_range(c, 0, c->staged.size());
+int ft_stage(ft_ctx* c, const ft_request* reqs, size_t batch) {
+  if (!c || (!reqs && batch)) return fail(FT_E_ARG, "ft_stage: null argument");
+  if (!c->reserved) return fail(FT_E_STATE, "ft_stage: init_tbs_gpu (ft_reserve) was not called");
+  if (batch == 0 || batch > c->max_staged)
+    return fail(FT_E_LIMIT, "ft_stage: batch size " + std::to_string(batch) +
+                                " not in [1, " + std::to_string(c->max_staged) + "]");
+  (void)hipSetDevice(c->device);
+  // the previous staging copy may still be queued behind a running launch:
+  // it reads h_stage, which is rewritten below
+  if (c->stage_pending) {
+    const hipError_t we = hipEventSynchronize(c->stage_ev);
+    if (we != hipSuccess) return hip_fail(we, "hipEventSynchronize(stage)");
+    c->stage_pending = false;
+  }
+  c->staged.assign(batch, StagedReq());
+  c->launched_slot.assign(batch, 0);
+  c->launched = false;
+  StageLimits lim{c->max_steps, c->max_topk, c->max_out_beams, c->max_out_tokens};
+  uint64_t used = 0;
+  if (int rc = pack_batch(reqs, batch, lim, c->h_stage, c->stage_cap, c->staged.data(),
+                          c->sort_tmp.data(), &used, &c->out_stride)) {
+    c->staged.clear();
+    c->launched_slot.clear();
+    return rc;
+  }
+  const uint64_t off = used;
+  hipError_t e = hipMemcpyAsync(c->d_stage, c->h_stage, off, hipMemcpyHostToDevice, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(stage)");
+  if ((e = hipEventRecord(c->stage_ev, c->stream)) != hipSuccess)
+    return hip_fail(e, "hipEventRecord(stage)");
+  c->stage_pending = true;
+  return FT_OK;
 }
 
-int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
-  if (!c) return fail(FT_E_ARG, "ft_launch_range: null context");
-  if (c->staged.empty()) return fail(FT_E_STATE, "ft_launch: nothing staged");
-  if (count == 0 || count > c->max_batch || first + count > c->staged.size())
-    return fail(FT_E_LIMIT, "ft_launch_range: [" + std::to_string(first) + ", +" +
-                                std::to_string(count) + ") exceeds the staged requests or max_batch_size " +
-                                std::to_string(c->max_batch));
+// Kernel arguments for requests [first, first + count) of a batch staged
+// at `stage` (DevReq array first), with workspace slots of `ws_stride`
+// bytes from `ws` and output blocks of `out_stride` bytes from `out`.
+static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, size_t count,
+                         uint32_t kmax, uint8_t* ws, uint64_t ws_stride, const WsLayout& lay,
+                         uint8_t* out, uint64_t out_stride) {
   KArgs a{};
   a.recs = (const ft_node_rec*)(c->d_image + c->hdr.recs_offset);
   a.parent = (const uint32_t*)(c->d_image + c->hdr.parent_offset);
   a.tail = (const uint32_t*)(c->d_image + c->hdr.tail_offset);
-  a.reqs = (const DevReq*)c->d_stage + first;
-  a.stage = c->d_stage;
-  a.ws = c->d_ws;
-  a.ws_stride = c->ws_stride;
-  a.out = c->d_out + first * c->out_stride;
-  a.out_stride = c->out_stride;
-  a.lay = c->lay;
+  a.reqs = (const DevReq*)stage + first;
+  a.stage = stage;
+  a.ws = ws;
+  a.ws_stride = ws_stride;
+  a.out = out + first * out_stride;
+  a.out_stride = out_stride;
+  a.lay = lay;
   a.batch = (uint32_t)count;
-  uint32_t kmax = 1;
-  for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
   const uint64_t sl = (uint64_t)c->scan_mult * kmax;
   a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
   // helpers per request: as many as stay co-resident with the batch
@@ -767,6 +921,12 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   a.labels = c->d_labels;
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
+  return a;
+}
+
+// One cooperative launch on the context stream, bracketed by a pair of the
+// ring's timing events.
+static int launch_timed(ft_ctx* c, const KArgs& a) {
   (void)hipSetDevice(c->device);
   const size_t slot = (c->launches % ft_ctx::kRing) * 2;
   (void)hipEventRecord(c->ring[slot], c->stream);
@@ -774,7 +934,28 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel");
   (void)hipEventRecord(c->ring[slot + 1], c->stream);
   ++c->launches;
+  return FT_OK;
+}
+
+int ft_launch(ft_ctx* c) {
+  if (!c) return fail(FT_E_ARG, "ft_launch: null context");
+  return ft_launch_range(c, 0, c->staged.size());
+}
+
+int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
+  if (!c) return fail(FT_E_ARG, "ft_launch_range: null context");
+  if (c->staged.empty()) return fail(FT_E_STATE, "ft_launch: nothing staged");
+  if (count == 0 || count > c->max_batch || first + count > c->staged.size())
+    return fail(FT_E_LIMIT, "ft_launch_range: [" + std::to_string(first) + ", +" +
+                                std::to_string(count) + ") exceeds the staged requests or max_batch_size " +
+                                std::to_string(c->max_batch));
+  uint32_t kmax = 1;
+  for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
+  const KArgs a = kernel_args(c, c->d_stage, first, count, kmax, c->d_ws, c->ws_stride,
+                              c->lay, c->d_out, c->out_stride);
+  if (int rc = launch_timed(c, a)) return rc;
   c->launched = true;
+  for (size_t i = first; i < first + count; ++i) c->launched_slot[i] = 1;
   return FT_OK;
 }
 
@@ -803,7 +984,9 @@ int ft_reserve_staging(ft_ctx* c, size_t max_staged) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   c->staged.clear();
+  c->launched_slot.clear();
   c->launched = false;
+  c->stage_pending = false;
   return alloc_staging(c, max_staged);
 }
 
@@ -823,30 +1006,34 @@ int ft_sync(ft_ctx* c, double* ms) {
   return FT_OK;
 }
 
-int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
-  if (!c) return fail(FT_E_ARG, "ft_fetch: null context");
-  if (!c->launched) return fail(FT_E_STATE, "ft_fetch: no launch to fetch");
-  if (batch != c->staged.size()) return fail(FT_E_ARG, "ft_fetch: batch mismatch");
-  (void)hipSetDevice(c->device);
-  hipError_t e = hipMemcpyAsync(c->h_out, c->d_out, c->out_stride * batch,
-                                hipMemcpyDeviceToHost, c->stream);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(output)");
-  double ms = 0.0;
-  int rc = ft_sync(c, &ms);
-  if (rc) return rc;
+// Fills `res` from the output blocks of a batch copied back to h_out
+// (out_stride bytes per request).  Returns the first request error.
+static int unpack_results(const uint8_t* h_out, uint64_t out_stride, const StagedReq* staged,
+                          const uint8_t* launched, size_t batch, ft_result* res,
+                          int wall_khz, double kernel_ms, ft_timing* timing) {
   int first_err = FT_OK;
   ft_timing tm{};
-  tm.kernel_ms = ms;
-  const double tick_ms = c->wall_khz > 0 ? 1.0 / c->wall_khz : 0.0;
+  tm.kernel_ms = kernel_ms;
+  const double tick_ms = wall_khz > 0 ? 1.0 / wall_khz : 0.0;
   for (size_t r = 0; r < batch; ++r) {
-    const StagedReq& st = c->staged[r];
+    const StagedReq& st = staged[r];
     ft_result& o = res[r];
+    if (!launched[r]) {
+      // staged but not launched since: d_out holds no result of this request
+      o.count = 0;
+      o.status = FT_E_STATE;
+      if (!first_err) {
+        first_err = FT_E_STATE;
+        g_err = "request " + std::to_string(r) + ": staged but not launched";
+      }
+      continue;
+    }
     if (st.skip) {
       o.count = 0;
       o.status = FT_OK;
       continue;
     }
-    const uint8_t* ob = c->h_out + c->out_stride * r;
+    const uint8_t* ob = h_out + out_stride * r;
     const OutHeader* oh = (const OutHeader*)ob;
     tm.expand_ms += oh->ticks_expand * tick_ms;
     tm.select_ms += oh->ticks_select * tick_ms;
@@ -902,6 +1089,21 @@ int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
   return first_err;
 }
 
+int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
+  if (!c) return fail(FT_E_ARG, "ft_fetch: null context");
+  if (!c->launched) return fail(FT_E_STATE, "ft_fetch: no launch to fetch");
+  if (batch != c->staged.size()) return fail(FT_E_ARG, "ft_fetch: batch mismatch");
+  (void)hipSetDevice(c->device);
+  hipError_t e = hipMemcpyAsync(c->h_out, c->d_out, c->out_stride * batch,
+                                hipMemcpyDeviceToHost, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(output)");
+  double ms = 0.0;
+  int rc = ft_sync(c, &ms);
+  if (rc) return rc;
+  return unpack_results(c->h_out, c->out_stride, c->staged.data(), c->launched_slot.data(),
+                        batch, res, c->wall_khz, ms, timing);
+}
+
 int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
               ft_result* results, ft_timing* timing) {
   int rc = ft_stage(c, reqs, batch);
@@ -923,6 +1125,7 @@ void ft_destroy(ft_ctx* c) {
   if (c->d_labels) (void)hipFree(c->d_labels);
   for (auto& ev : c->ring)
     if (ev) (void)hipEventDestroy(ev);
+  if (c->stage_ev) (void)hipEventDestroy(c->stage_ev);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }

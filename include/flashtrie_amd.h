@@ -141,7 +141,11 @@ typedef struct ft_timing {
 
 typedef struct ft_ctx ft_ctx;
 
-/* Uploads a trie image (ft_image_header + arrays) to device `device`. */
+/* Uploads a trie image (ft_image_header + arrays) to device `device`.
+ * The whole image is validated on the host first (BFS child ranges, parent
+ * links, edge lengths and depths, sibling order, token ids < 2^31 - 1, tail
+ * bounds, key count); a malformed image returns FT_E_IMAGE before any
+ * device call. */
 int ft_create(const void* image, size_t image_bytes, int device,
               ft_ctx** out);
 
@@ -154,7 +158,10 @@ int ft_reserve(ft_ctx* ctx, size_t max_batch, size_t max_topk,
                size_t max_out_tokens, size_t max_inter_beams);
 
 /* Validates and packs `batch` requests into pinned memory and copies them to
- * the device workspace (async on the context stream). */
+ * the device workspace (async on the context stream).  It first waits for
+ * the previous staging copy, which may still be queued behind a running
+ * launch, so the pinned buffer is never rewritten under it.  Staging starts
+ * a new batch: results of earlier launches can no longer be fetched. */
 int ft_stage(ft_ctx* ctx, const ft_request* reqs, size_t batch);
 
 /* Launches the search kernel over the staged batch (async); at most
@@ -174,7 +181,10 @@ int ft_launch_range(ft_ctx* ctx, size_t first, size_t count);
  * waits for the stream.  At most 1024 are kept. */
 int ft_launch_times(ft_ctx* ctx, double* ms, size_t n);
 
-/* Waits for the last launch, copies results back, fills `results`. */
+/* Waits for the last launch, copies results back, fills `results`.  A
+ * staged request that no ft_launch / ft_launch_range has covered since the
+ * last ft_stage gets status FT_E_STATE and count 0 (the call then returns
+ * FT_E_STATE); it never returns another launch's output. */
 int ft_fetch(ft_ctx* ctx, ft_result* results, size_t batch,
              ft_timing* timing);
 

@@ -146,6 +146,7 @@ def test_build_invariants(po, keys):
     n = len(term)
     assert cb[0] == min(1, n) or n == 1
     assert cb[-1] == n
+    assert all(cb[v] <= cb[v + 1] for v in range(n))  # breadth-first ids
     for v in range(n):
         kids = list(range(cb[v], cb[v + 1]))
         assert all(c > v for c in kids)
@@ -153,6 +154,13 @@ def test_build_invariants(po, keys):
         assert firsts == sorted(set(firsts))   # label order, distinct
         for c in kids:
             assert len(edges[c]) >= 1
+        # maximal path compression (louds-trie.cc:537-550): an edge stops
+        # only where a key ends or the keys below it branch, so a non-root
+        # node that ends no key has at least two children (a single child
+        # would have been merged into its edge, and a childless one would
+        # be a key)
+        if v > 0 and not term[v]:
+            assert len(kids) >= 2, (v, edges[v], kids)
     for k in uniq:
         node = _walk(cb, edges, list(k))
         assert node is not None and term[node] == 1
