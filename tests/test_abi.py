@@ -99,29 +99,11 @@ def test_create_rejects_corrupt_images_before_any_device_call(ft):
 
 # ---- the C ABI driven from ctypes, as the integration guide shows ---------
 
-class Request(ctypes.Structure):
-    _fields_ = [("beams", ctypes.POINTER(ctypes.c_uint32)), ("num_beams", ctypes.c_uint32),
-                ("num_steps", ctypes.c_uint32), ("topk", ctypes.c_uint32),
-                ("topk_id", ctypes.POINTER(ctypes.c_uint32)),
-                ("topk_logp", ctypes.POINTER(ctypes.c_float)),
-                ("topk_id_rows", ctypes.c_void_p), ("topk_logp_rows", ctypes.c_void_p),
-                ("token_logp_threshold", ctypes.c_float),
-                ("sent_logp_threshold", ctypes.c_double),
-                ("length_norm", ctypes.c_double), ("early_exit", ctypes.c_int)]
-
-
-class Result(ctypes.Structure):
-    _fields_ = [("capacity", ctypes.c_uint32), ("token_stride", ctypes.c_uint32),
-                ("count", ctypes.c_uint32), ("status", ctypes.c_int32),
-                ("logp_norm", ctypes.POINTER(ctypes.c_double)),
-                ("length", ctypes.POINTER(ctypes.c_uint32)),
-                ("tokens", ctypes.POINTER(ctypes.c_uint32)),
-                ("device_ms", ctypes.c_double * 4),
-                ("step_stats", ctypes.POINTER(ctypes.c_uint64))]
+from cabi import Request, Result  # noqa: E402
 
 
 def test_struct_layouts_match_the_header(tmp_path):
-    # the ctypes mirrors above against what a C compiler makes of the header
+    # the ctypes mirrors against what a C compiler makes of the header
     # (sizeof and every field offset of ft_request and ft_result)
     import subprocess
     fields = {"ft_request": [f for f, _ in Request._fields_],
@@ -142,85 +124,3 @@ def test_struct_layouts_match_the_header(tmp_path):
         assert int(out[st]) == ctypes.sizeof(cls), st
         for f in fields[st]:
             assert int(out[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
-
-
-def _bind(lib):
-    lib.ft_create.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
-                              ctypes.POINTER(ctypes.c_void_p)]
-    lib.ft_reserve.argtypes = [ctypes.c_void_p] + [ctypes.c_size_t] * 6
-    lib.ft_search.argtypes = [ctypes.c_void_p, ctypes.POINTER(Request), ctypes.c_size_t,
-                              ctypes.POINTER(Result), ctypes.c_void_p]
-    lib.ft_stage.argtypes = [ctypes.c_void_p, ctypes.POINTER(Request), ctypes.c_size_t]
-    lib.ft_launch_range.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t]
-    lib.ft_fetch.argtypes = [ctypes.c_void_p, ctypes.POINTER(Result), ctypes.c_size_t,
-                             ctypes.c_void_p]
-    lib.ft_destroy.argtypes = [ctypes.c_void_p]
-    lib.ft_last_error.restype = ctypes.c_char_p
-
-
-@pytest.mark.gpu
-def test_c_abi_search_through_ctypes(ft, po):
-    lib = ctypes.CDLL(LIB)
-    _bind(lib)
-
-    def check(rc):
-        if rc != 0:
-            raise RuntimeError(lib.ft_last_error().decode())
-
-    toks, offs = ft.synth_keys(30000, 4096, 3, 8, 1.1, 21)
-    t = ft.Trie()
-    t.build_arrays(toks, offs)
-    image = np.array(t.image(), dtype=np.uint8)
-    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
-    B, T, K, F, n = 16, 8, 32, 16, 4
-    ids, lp = ft.synth_requests(t, 0, n, 4096, T, K, B, 0.3, 2.0, True, 21, model=1)
-    ids = np.ascontiguousarray(ids)
-    lp = np.ascontiguousarray(lp)
-    beams = np.full((n, T), B, dtype=np.uint32)
-    ctx = ctypes.c_void_p()
-    check(lib.ft_create(image.ctypes.data, image.nbytes, 0, ctypes.byref(ctx)))
-    try:
-        check(lib.ft_reserve(ctx, n, K, T, B, B * T, 4096))
-        reqs = (Request * n)()
-        for i in range(n):
-            r = reqs[i]
-            r.beams = beams[i].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-            r.num_beams = T
-            r.num_steps = T
-            r.topk = K
-            r.topk_id = ids[i].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-            r.topk_logp = lp[i].ctypes.data_as(ctypes.POINTER(ctypes.c_float))
-            r.token_logp_threshold = -10.0
-            r.sent_logp_threshold = -40.0
-            r.length_norm = 5.0
-            r.early_exit = int(i % 2)
-        norms = np.zeros((n, F), dtype=np.float64)
-        lens = np.zeros((n, F), dtype=np.uint32)
-        otok = np.zeros((n, F, T), dtype=np.uint32)
-        res = (Result * n)()
-        for i in range(n):
-            res[i].capacity = F
-            res[i].token_stride = T
-            res[i].logp_norm = norms[i].ctypes.data_as(ctypes.POINTER(ctypes.c_double))
-            res[i].length = lens[i].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-            res[i].tokens = otok[i].ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-        print("ctypes ft_search batch", n, flush=True)
-        check(lib.ft_search(ctx, reqs, n, res, None))
-        for i in range(n):
-            want = o.tbs(beams[i], ids[i], lp[i], -10.0, -40.0, 5.0, bool(i % 2))
-            c = res[i].count
-            assert res[i].status == 0
-            got = [otok[i, j, :lens[i, j]].tolist() for j in range(c)]
-            assert got == want[0], i
-            assert np.array_equal(norms[i, :c], want[1]), i
-        # a staged request that no launch covered comes back FT_E_STATE
-        check(lib.ft_stage(ctx, reqs, n))
-        check(lib.ft_launch_range(ctx, 0, 2))
-        rc = lib.ft_fetch(ctx, res, n, None)
-        assert rc == -5, rc
-        assert [res[i].status for i in range(n)] == [0, 0, -5, -5]
-        want = o.tbs(beams[1], ids[1], lp[1], -10.0, -40.0, 5.0, True)
-        c = res[1].count
-        assert [otok[1, j, :lens[1, j]].tolist() for j in range(c)] == want[0]
-    finally:
-        lib.ft_destroy(ctx)

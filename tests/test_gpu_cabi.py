@@ -1,0 +1,48 @@
+"""The C ABI driven from ctypes, as another host language would: ft_create,
+ft_reserve, ft_search, and ft_stage / ft_launch_range / ft_fetch, against the
+oracle.  (This module sorts after the command line tool's test: once this
+process has made cooperative launches, another process cannot.)"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from cabi import Batch, check, load
+
+
+@pytest.mark.gpu
+def test_c_abi_search_through_ctypes(ft, po):
+    lib = load()
+    toks, offs = ft.synth_keys(30000, 4096, 3, 8, 1.1, 21)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    image = np.array(t.image(), dtype=np.uint8)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    B, T, K, F, n = 16, 8, 32, 16, 4
+    ids, lp = ft.synth_requests(t, 0, n, 4096, T, K, B, 0.3, 2.0, True, 21, model=1)
+    beams = np.full((n, T), B, dtype=np.uint32)
+    early = [i % 2 for i in range(n)]
+    b = Batch(beams, ids, lp, -10.0, -40.0, 5.0, early, F)
+    ctx = ctypes.c_void_p()
+    check(lib, lib.ft_create(image.ctypes.data, image.nbytes, 0, ctypes.byref(ctx)))
+    try:
+        check(lib, lib.ft_reserve(ctx, n, K, T, B, B * T, 4096))
+        print("ctypes ft_search batch", n, flush=True)
+        check(lib, lib.ft_search(ctx, b.reqs, n, b.res, None))
+        for i in range(n):
+            want = o.tbs(beams[i], ids[i], lp[i], -10.0, -40.0, 5.0, bool(early[i]))
+            got = b.results(i)
+            assert b.res[i].status == 0
+            assert got[0] == want[0], i
+            assert np.array_equal(got[1], want[1]), i
+        # a staged request that no launch covered comes back FT_E_STATE
+        check(lib, lib.ft_stage(ctx, b.reqs, n))
+        check(lib, lib.ft_launch_range(ctx, 0, 2))
+        rc = lib.ft_fetch(ctx, b.res, n, None)
+        assert rc == -5, rc
+        assert [b.res[i].status for i in range(n)] == [0, 0, -5, -5]
+        want = o.tbs(beams[1], ids[1], lp[1], -10.0, -40.0, 5.0, True)
+        assert b.results(1)[0] == want[0]
+    finally:
+        lib.ft_destroy(ctx)
