@@ -16,6 +16,7 @@
 #include <cstring>
 #include <limits>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -24,6 +25,8 @@
 #include "tbs_kernel.h"
 
 using namespace ftk;
+
+static_assert(kScratchBytes == FT_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");
 
 namespace {
 
@@ -102,6 +105,10 @@ struct ft_ctx {
                               // a lone request gets every CU)
   uint32_t share_min = 4096;  // work items from which a step is shared
   int max_resident = 0;
+  // this device's no-allocation scratch (looked up at ft_create), or null
+  // with the reason in scratch_err
+  uint8_t* d_scratch = nullptr;
+  std::string scratch_err;
   // ring of (start, end) event pairs, one pair per launch
   static constexpr size_t kRing = 1024;
   std::vector<hipEvent_t> ring;
@@ -527,6 +534,13 @@ int ft_create(const void* image, size_t image_bytes, int device,
   (void)hipDeviceGetAttribute(&wc, hipDeviceAttributeWallClockRate, device);
   c->wall_khz = wc;
   std::snprintf(c->name, sizeof(c->name), "%s", prop.gcnArchName);
+  {
+    // the no-allocation scratch of this device (the device is current)
+    void* sp = nullptr;
+    const hipError_t se = scratch_address(device, &sp);
+    if (se == hipSuccess) c->d_scratch = (uint8_t*)sp;
+    else c->scratch_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se);
+  }
   if ((e = hipMalloc(&c->d_image, image_bytes)) != hipSuccess) {
     delete c;
     return hip_fail(e, "hipMalloc(image)");
@@ -1111,6 +1125,81 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
   rc = ft_launch(c);
   if (rc) return rc;
   return ft_fetch(c, results, batch, timing);
+}
+
+// Host side of the no-allocation path: pageable buffers in the library's
+// own static storage (no allocation), used under g_noalloc_mu.
+namespace {
+constexpr size_t kNoAllocMaxBatch = 64;
+constexpr uint64_t kNoAllocHostBytes = 16ull << 20;
+std::mutex g_noalloc_mu;
+alignas(256) uint8_t g_na_stage[kNoAllocHostBytes];
+alignas(256) uint8_t g_na_out[kNoAllocHostBytes];
+StagedReq g_na_staged[kNoAllocMaxBatch];
+uint8_t g_na_launched[kNoAllocMaxBatch];
+std::pair<uint32_t, uint32_t> g_na_sort[kMaxLdsTopk];
+}  // namespace
+
+int ft_search_noalloc(ft_ctx* c, const ft_request* reqs, size_t batch,
+                      ft_result* results, ft_timing* timing) {
+  if (!c || !reqs || !results) return fail(FT_E_ARG, "ft_search_noalloc: null argument");
+  if (batch == 0 || batch > kNoAllocMaxBatch)
+    return fail(FT_E_LIMIT, "ft_search_noalloc: batch size " + std::to_string(batch) +
+                                " not in [1, " + std::to_string(kNoAllocMaxBatch) + "]");
+  if (!c->d_scratch)
+    return fail(FT_E_STATE, "ft_search_noalloc: no scratch on this device (" +
+                                c->scratch_err + ")");
+  // one call at a time in this process: the scratch and the host buffers
+  // are shared by every call
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  (void)hipSetDevice(c->device);
+  for (size_t r = 0; r < batch; ++r) {
+    g_na_staged[r] = StagedReq();
+    g_na_launched[r] = 1;
+  }
+  const StageLimits lim{16383, kMaxLdsTopk, kMaxBeams, ~0ull};
+  uint64_t used = 0, out_stride = 0;
+  if (int rc = pack_batch(reqs, batch, lim, g_na_stage, kNoAllocHostBytes, g_na_staged,
+                          g_na_sort, &used, &out_stride))
+    return rc;
+  // the workspace this batch needs: its widest beam, longest row and
+  // largest history (the sum of a request's beam widths bounds its records)
+  uint64_t B = 1, K = 1, H = 1;
+  for (size_t r = 0; r < batch; ++r) {
+    const StagedReq& st = g_na_staged[r];
+    if (st.skip) continue;
+    B = std::max(B, st.bmax);
+    K = std::max<uint64_t>(K, st.K);
+    H = std::max(H, st.hsum);
+  }
+  if (B * K + B >= 0xFFFFFFF0ull || H >= 0xFFFFFFF0ull)
+    return fail(FT_E_LIMIT, "ft_search_noalloc: beams * topk too large");
+  WsLayout L{};
+  const uint64_t ws_stride = ws_layout(B, K, H, &L);
+  const uint64_t out_off = align_up(used, 256);
+  const uint64_t ws_off = align_up(out_off + out_stride * batch, 256);
+  const uint64_t total = ws_off + ws_stride * batch;
+  if (total > kScratchBytes || out_stride * batch > kNoAllocHostBytes)
+    return fail(FT_E_LIMIT, "ft_search_noalloc: the batch needs " + std::to_string(total) +
+                                " bytes of device scratch (limit " +
+                                std::to_string(kScratchBytes) + ")");
+  uint8_t* base = c->d_scratch;
+  hipError_t e = hipMemcpyAsync(base, g_na_stage, used, hipMemcpyHostToDevice, c->stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(scratch stage)");
+  // the control blocks start at "nothing posted" (a fill kernel, no memset)
+  if ((e = clear_controls(base + ws_off, ws_stride, L.ctl, (uint32_t)batch, c->stream)) !=
+      hipSuccess)
+    return hip_fail(e, "clear_controls");
+  const KArgs a = kernel_args(c, base, 0, batch, (uint32_t)K, base + ws_off, ws_stride, L,
+                              base + out_off, out_stride);
+  if (int rc = launch_timed(c, a)) return rc;
+  if ((e = hipMemcpyAsync(g_na_out, base + out_off, out_stride * batch, hipMemcpyDeviceToHost,
+                          c->stream)) != hipSuccess)
+    return hip_fail(e, "hipMemcpyAsync(scratch output)");
+  double ms = 0.0;
+  if (int rc = ft_sync(c, &ms)) return rc;
+  return unpack_results(g_na_out, out_stride, g_na_staged, g_na_launched, batch, results,
+                        c->wall_khz, ms, timing);
 }
 
 void ft_destroy(ft_ctx* c) {

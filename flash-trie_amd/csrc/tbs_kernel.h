@@ -207,6 +207,21 @@ struct KArgs {
 // cooperative launch on `stream`.
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
 
+// The no-allocation scratch: one file-scope device array of this many
+// bytes per device, holding a search's staged requests, outputs and
+// workspace slots when the caller cannot allocate.
+constexpr uint64_t kScratchBytes = 128ull << 20;
+
+// Device address of the scratch array on `device`, which must be the
+// current device.  Looked up once per device (hipGetSymbolAddress) and
+// kept; later calls return the kept address.
+hipError_t scratch_address(int device, void** ptr);
+
+// Zeroes the control block (Ctl, at byte ctl_off) of `count` workspace
+// slots of `stride` bytes from `ws`, with a fill kernel on `stream`.
+hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint32_t count,
+                          hipStream_t stream);
+
 // Workgroups of the search kernel that fit on the device at once.
 int tbs_max_resident_blocks(int num_cus);
 

@@ -37,6 +37,8 @@
 
 #include <stdint.h>
 
+#include <mutex>
+
 #include "tbs_kernel.h"
 
 namespace ftk {
@@ -1901,6 +1903,51 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     oh->children = sm.cnt_children;
     oh->probes = sm.cnt_probes;
   }
+}
+
+// The no-allocation scratch (kScratchBytes per device, held from the first
+// use of the library on a device until the process ends).  Host code never
+// passes `scratch` itself to a kernel or a copy -- on the host the name is
+// a stand-in, not a device address -- only the address scratch_address()
+// looked up for the device.
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t scratch_address(int device, void** ptr) {
+  if (device < 0 || device >= kMaxDevices || !ptr) return hipErrorInvalidValue;
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  if (cur != device) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_ptr[device] = p;
+  }
+  *ptr = g_scratch_ptr[device];
+  return hipSuccess;
+}
+
+// One workgroup per slot: the slot's control block, word by word.
+__global__ void __launch_bounds__(128) clear_ctl_kernel(uint8_t* ws, uint64_t stride,
+                                                        uint64_t ctl_off) {
+  uint32_t* p = (uint32_t*)(ws + (uint64_t)blockIdx.x * stride + ctl_off);
+  for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(Ctl) / 4); i += blockDim.x) p[i] = 0u;
+}
+
+hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint32_t count,
+                          hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  hipLaunchKernelGGL(clear_ctl_kernel, dim3(count), dim3(128), 0, stream, ws, stride, ctl_off);
+  return hipGetLastError();
 }
 
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
