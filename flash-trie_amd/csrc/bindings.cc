@@ -256,6 +256,116 @@ PYBIND11_MODULE(flashtrie, m) {
   m.def("load_topk_keys_and_scores", &marisa::load_topk_keys_and_scores,
         py::arg("dataset_dir"));
 
+  // ---- the reference's timing boundary, driven from C++ ----------------------
+  m.def(
+      "bench_boundary",
+      [](Trie& trie, py::array_t<uint32_t, py::array::c_style | py::array::forcecast> beams,
+         py::array_t<uint32_t, py::array::c_style | py::array::forcecast> ids,
+         py::array_t<float, py::array::c_style | py::array::forcecast> logp, size_t batch,
+         float token_logp_threshold, double sent_logp_threshold, double length_norm,
+         bool early_exit, int warmup_passes, int passes) {
+        // Consecutive batches of `batch` requests, each converted to
+        // TbsInput vectors (untimed, as the module converts Python lists
+        // before its timer) and searched by Trie::tbs_gpu_batched; the call
+        // is timed with steady_clock exactly where bs_tbs_gpu times it
+        // (tools/bindings.cpp:90-100): staging, H2D, the launch, D2H and the
+        // filled output vectors.  Returns (call_ms[passes][calls],
+        // pass_s[passes] -- wall time of each measured pass, conversions
+        // included -- and, for every request of the last pass, its result
+        // count and an FNV-1a hash over 32-bit words of (count, then per
+        // result: length, tokens, the two words of the norm)).
+        if (beams.ndim() != 2 || ids.ndim() != 3 || logp.ndim() != 3 ||
+            ids.shape(0) != beams.shape(0) || ids.shape(1) != beams.shape(1) ||
+            logp.shape(0) != ids.shape(0) || logp.shape(1) != ids.shape(1) ||
+            logp.shape(2) != ids.shape(2))
+          throw marisa::Exception(MARISA_CODE_ERROR,
+                                  "bench_boundary: shapes must be [n][T], [n][T][K]");
+        if (batch == 0 || passes < 1 || warmup_passes < 0)
+          throw marisa::Exception(MARISA_CODE_ERROR, "bench_boundary: bad batch or passes");
+        const size_t n = beams.shape(0), T = beams.shape(1), K = ids.shape(2);
+        const size_t calls = n / batch;
+        if (calls == 0)
+          throw marisa::Exception(MARISA_CODE_ERROR, "bench_boundary: fewer requests than batch");
+        py::array_t<double> call_ms({(py::ssize_t)passes, (py::ssize_t)calls});
+        py::array_t<double> pass_s((py::ssize_t)passes);
+        py::array_t<uint32_t> counts((py::ssize_t)(calls * batch));
+        py::array_t<uint64_t> hashes((py::ssize_t)(calls * batch));
+        const uint32_t* bp = beams.data();
+        const uint32_t* ip = ids.data();
+        const float* lp = logp.data();
+        double* cm = call_ms.mutable_data();
+        double* ps = pass_s.mutable_data();
+        uint32_t* cp = counts.mutable_data();
+        uint64_t* hp = hashes.mutable_data();
+        {
+          py::gil_scoped_release nogil;
+          using clk = std::chrono::steady_clock;
+          std::vector<std::vector<uint32_t>> bb(batch);
+          std::vector<std::vector<std::vector<Label>>> tid(batch);
+          std::vector<std::vector<std::vector<float>>> tlp(batch);
+          std::vector<std::vector<std::vector<Label>>> out_sent(batch);
+          std::vector<std::vector<double>> out_norm(batch);
+          for (int p = 0; p < warmup_passes + passes; ++p) {
+            const bool measured = p >= warmup_passes;
+            const auto p0 = clk::now();
+            for (size_t c = 0; c < calls; ++c) {
+              std::vector<TbsInput> inputs;
+              inputs.reserve(batch);
+              for (size_t i = 0; i < batch; ++i) {
+                const size_t r = c * batch + i;
+                bb[i].assign(bp + r * T, bp + (r + 1) * T);
+                tid[i].resize(T);
+                tlp[i].resize(T);
+                for (size_t t = 0; t < T; ++t) {
+                  tid[i][t].assign(ip + (r * T + t) * K, ip + (r * T + t + 1) * K);
+                  tlp[i][t].assign(lp + (r * T + t) * K, lp + (r * T + t + 1) * K);
+                }
+                out_sent[i].clear();
+                out_norm[i].clear();
+                inputs.push_back(TbsInput{bb[i], tid[i], tlp[i], out_sent[i], out_norm[i],
+                                          token_logp_threshold, sent_logp_threshold,
+                                          length_norm, early_exit});
+              }
+              const auto t0 = clk::now();
+              trie.tbs_gpu_batched(inputs);
+              const auto t1 = clk::now();
+              if (measured)
+                cm[(size_t)(p - warmup_passes) * calls + c] =
+                    std::chrono::duration<double, std::milli>(t1 - t0).count();
+              if (p == warmup_passes + passes - 1) {
+                for (size_t i = 0; i < batch; ++i) {
+                  uint64_t h = 0xcbf29ce484222325ull;
+                  auto mix = [&h](uint32_t w) {
+                    h ^= w;
+                    h *= 0x100000001b3ull;
+                  };
+                  const auto& os = out_sent[i];
+                  mix((uint32_t)os.size());
+                  for (size_t j = 0; j < os.size(); ++j) {
+                    mix((uint32_t)os[j].size());
+                    for (Label tk : os[j]) mix(tk);
+                    uint64_t bits;
+                    std::memcpy(&bits, &out_norm[i][j], 8);
+                    mix((uint32_t)bits);
+                    mix((uint32_t)(bits >> 32));
+                  }
+                  cp[c * batch + i] = (uint32_t)os.size();
+                  hp[c * batch + i] = h;
+                }
+              }
+            }
+            if (measured)
+              ps[p - warmup_passes] =
+                  std::chrono::duration<double>(clk::now() - p0).count();
+          }
+        }
+        return py::make_tuple(call_ms, pass_s, counts, hashes);
+      },
+      py::arg("trie"), py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"),
+      py::arg("batch"), py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
+      py::arg("length_norm"), py::arg("early_exit"), py::arg("warmup_passes") = 1,
+      py::arg("passes") = 2);
+
   // ---- numpy batch path: stage / launch / sync / fetch -----------------------
   m.def(
       "stage",
@@ -405,7 +515,10 @@ PYBIND11_MODULE(flashtrie, m) {
   m.def(
       "synth_paper_trie",
       [](Trie& trie, uint64_t n_keys, uint32_t vocab, double s, uint64_t seed,
-         uint32_t lmin, uint32_t lmax, double p_end, int threads) {
+         uint32_t lmin, uint32_t lmax, double p_end, int threads, uint64_t unique_keys) {
+        // n_keys independent draws; with unique_keys > 0 the trie is then
+        // topped up to exactly that many unique keys (prefix keys of length
+        // >= lmin, see add_prefix_keys)
         ftamd::ImageBlob img;
         std::string err;
         bool ok;
@@ -413,6 +526,8 @@ PYBIND11_MODULE(flashtrie, m) {
           py::gil_scoped_release nogil;
           ok = ftamd::synth::make_paper_trie(n_keys, vocab, s, lmin, lmax, p_end,
                                              seed, threads, &img, &err);
+          if (ok && unique_keys)
+            ok = ftamd::synth::add_prefix_keys(&img, unique_keys, lmin, seed, threads, &err);
         }
         if (!ok) throw marisa::Exception(MARISA_SIZE_ERROR, "synth_paper_trie: " + err);
         marisa::TrieImpl* im = trie.impl();
@@ -421,7 +536,7 @@ PYBIND11_MODULE(flashtrie, m) {
       },
       py::arg("trie"), py::arg("n_keys"), py::arg("vocab"), py::arg("s"),
       py::arg("seed"), py::arg("lmin") = 3, py::arg("lmax") = 16,
-      py::arg("p_end") = 0.25, py::arg("threads") = 0);
+      py::arg("p_end") = 0.25, py::arg("threads") = 0, py::arg("unique_keys") = 0);
   m.def(
       "validate_image",
       [](const Trie& trie) {

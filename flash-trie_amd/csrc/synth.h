@@ -96,5 +96,13 @@ bool make_paper_trie(uint64_t n_keys, uint32_t vocab, double zipf_s,
                      uint32_t lmin, uint32_t lmax, double p_end, uint64_t seed,
                      int threads, ImageBlob* out, std::string* err);
 
+// Makes the trie hold exactly `target_keys` keys by adding keys that are
+// prefixes of existing ones: the internal nodes (>= 2 children, no key
+// ending there, string depth >= min_depth) with the lowest seeded hash of
+// their node id become terminal.  The structure and node ids do not change.
+// For topping up a generated trie to an exact unique-key count.
+bool add_prefix_keys(ImageBlob* img, uint64_t target_keys, uint32_t min_depth,
+                     uint64_t seed, int threads, std::string* err);
+
 }  // namespace synth
 }  // namespace ftamd

@@ -530,5 +530,73 @@ bool make_paper_trie(uint64_t n_keys, uint32_t vocab, double zipf_s,
   return true;
 }
 
+bool add_prefix_keys(ImageBlob* img, uint64_t target_keys, uint32_t min_depth,
+                     uint64_t seed, int threads, std::string* err) {
+  ft_image_header& h = img->header();
+  if (h.num_keys > target_keys) {
+    *err = "the trie already holds more than the target number of keys";
+    return false;
+  }
+  const uint64_t need = target_keys - h.num_keys;
+  if (need == 0) return true;
+  if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+  const uint64_t N = h.num_nodes;
+  ft_node_rec* R = img->recs();
+  // a candidate is a node that no key ends at but keys continue below (>= 2
+  // children), whose string is at least min_depth tokens long; its rank is a
+  // seeded hash of its id, and the `need` lowest ranks become keys
+  auto cand = [&](uint64_t v) {
+    const uint32_t m = R[v].meta;
+    return v > 0 && !(m & FT_META_TERMINAL) && R[v + 1].child_begin > R[v].child_begin &&
+           (m & FT_META_DEPTH_MASK) >= min_depth;
+  };
+  auto rank = [&](uint64_t v) { return mix64(seed ^ mix64(v + 0x70F0ull)); };
+  auto parallel = [&](auto&& body) {
+    std::vector<std::thread> pool;
+    for (int w = 0; w < threads; ++w)
+      pool.emplace_back([&, w]() { body(N * w / threads, N * (w + 1) / threads, w); });
+    for (auto& th : pool) th.join();
+  };
+  // histogram of the top 16 bits of the ranks
+  constexpr int kBins = 1 << 16;
+  std::vector<std::vector<uint64_t>> hist(threads, std::vector<uint64_t>(kBins, 0));
+  parallel([&](uint64_t b, uint64_t e, int w) {
+    for (uint64_t v = b; v < e; ++v)
+      if (cand(v)) ++hist[w][rank(v) >> 48];
+  });
+  uint64_t cum = 0, rem = 0;
+  int cut = -1;
+  for (int k = 0; k < kBins && cut < 0; ++k) {
+    uint64_t c = 0;
+    for (int w = 0; w < threads; ++w) c += hist[w][k];
+    if (cum + c >= need) {
+      cut = k;
+      rem = need - cum;
+    } else {
+      cum += c;
+    }
+  }
+  if (cut < 0) {
+    *err = "not enough internal nodes to add the requested keys";
+    return false;
+  }
+  // in the cut bin, the `rem` lowest ranks (ties broken by node id)
+  std::vector<std::vector<std::pair<uint64_t, uint32_t>>> inbin(threads);
+  parallel([&](uint64_t b, uint64_t e, int w) {
+    for (uint64_t v = b; v < e; ++v)
+      if (cand(v) && (int)(rank(v) >> 48) == cut) inbin[w].push_back({rank(v), (uint32_t)v});
+  });
+  std::vector<std::pair<uint64_t, uint32_t>> bin;
+  for (auto& x : inbin) bin.insert(bin.end(), x.begin(), x.end());
+  std::sort(bin.begin(), bin.end());
+  for (uint64_t i = 0; i < rem; ++i) R[bin[i].second].meta |= FT_META_TERMINAL;
+  parallel([&](uint64_t b, uint64_t e, int) {
+    for (uint64_t v = b; v < e; ++v)
+      if (cand(v) && (int)(rank(v) >> 48) < cut) R[v].meta |= FT_META_TERMINAL;
+  });
+  h.num_keys = target_keys;
+  return true;
+}
+
 }  // namespace synth
 }  // namespace ftamd

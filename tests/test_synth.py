@@ -78,3 +78,42 @@ def test_synth_requests_rows_sorted_and_valid(ft):
         ids2, lp2 = ft.synth_requests(t, 0, 8, 4096, 8, 64, 16, 0.3, 2.0, True,
                                       5, threads=1, model=model)
         assert np.array_equal(ids, ids2) and np.array_equal(lp, lp2)
+
+
+def test_paper_trie_topped_up_to_exact_unique_keys(ft):
+    # draws give some number of unique keys; unique_keys tops the trie up to
+    # exactly that many by making internal nodes (>= 2 children, string depth
+    # >= lmin) terminal -- prefix keys -- without changing the structure
+    base = ft.Trie()
+    ft.synth_paper_trie(base, 30000, 5000, 1.05, 7)
+    t = ft.Trie()
+    want = base.num_keys() + 123
+    ft.synth_paper_trie(t, 30000, 5000, 1.05, 7, unique_keys=want)
+    ft.validate_image(t)
+    assert t.num_keys() == want
+    n, r0, p0, tl0 = decode_image(base.image())
+    n1, r1, p1, tl1 = decode_image(t.image())
+    assert n == n1 and np.array_equal(p0, p1) and np.array_equal(tl0, tl1)
+    for f in ("child_begin", "first_tok", "tail_off"):
+        assert np.array_equal(r0[f], r1[f])
+    m0, m1 = r0["meta"][:n], r1["meta"][:n]
+    added = np.nonzero((m1 >> 31) & ~(m0 >> 31) & 1)[0]
+    assert len(added) == 123
+    assert np.array_equal(m0 & 0x7FFFFFFF, m1 & 0x7FFFFFFF)
+    deg = np.diff(r0["child_begin"].astype(np.int64))[:n]
+    assert (deg[added] >= 2).all() and ((m0[added] & 0xFFFF) >= 3).all()
+    # the keys really are the old ones plus the added prefixes, all distinct,
+    # and the builder makes the same image from them
+    keys = _keys_of(t.image())
+    assert len(keys) == len({tuple(k) for k in keys}) == want
+    u = ft.Trie()
+    u.build(keys)
+    assert np.array_equal(t.image(), u.image())
+    # seeded: the same call gives the same trie; a target below the count is
+    # an error
+    t2 = ft.Trie()
+    ft.synth_paper_trie(t2, 30000, 5000, 1.05, 7, unique_keys=want)
+    assert np.array_equal(t.image(), t2.image())
+    with pytest.raises(RuntimeError, match="more than the target"):
+        ft.synth_paper_trie(ft.Trie(), 30000, 5000, 1.05, 7,
+                            unique_keys=base.num_keys() - 1)
