@@ -1,29 +1,45 @@
 #!/usr/bin/env python3
 """Trie beam search benchmark on one MI355X.
 
-A step is one launch of the search kernel over one batch of requests whose
-inputs are already resident in HBM.  Per batch size b in {1, 2, 4, 8} the
-benchmark runs W untimed and K timed launches over a pool of seeded
-synthetic requests, and reports:
+The headline is measured at the reference's timing boundary: C++ wall time
+around Trie::tbs_gpu_batched (staging, H2D, the search kernel, D2H and the
+filled output vectors), which is where the reference's bs_tbs_gpu starts and
+stops its clock (tools/bindings.cpp:90-100).  The protocol is the
+reference's (examples/flashtrie_bench.py:270-291): per configuration one
+warm-up pass and --passes measured passes over --requests seeded synthetic
+requests, statistics computed within each pass and averaged across passes.
 
-  value         peak requests/s over the batch sizes (device-resident)
-  latency_ms    batch-1 kernel latency (HIP events): mean and p99, plus the
-                same through the C++ boundary (host arrays in, results out)
-  roofline      algorithmic bytes per launch / average launch duration,
-                against the 8 TB/s HBM peak
+  value         peak requests/s over batch sizes 1, 2, 4, 8 at beam 1000
+                (requests of a pass / the sum of its boundary call times)
+  latency_ms    batch-1 boundary latency at beam 1000: mean and p99
+  boundary      the same sweep per proposal model and beam width, plus
+                harness wall q/s (Python lists built per batch and
+                bs_tbs_gpu, as examples/run_trie_search.py:189-199 times it)
+  device_resident  kernel-only figures (inputs already in HBM, HIP events)
+  roofline      algorithmic bytes per launch / average launch duration of
+                the search kernel against the 8 TB/s HBM peak
   cpu_baseline  the CPU oracle (a restatement of the reference's
                 LoudsTrie::tbs) on the host cores, on a bounded sample
 
-Workloads (see --config):
-  paper  synthetic 800M-key trie over a 2.2M-token vocabulary, key length
-         3-16 (mean ~6), Zipf(1.05) prefix sharing; beam = K = 1000, 16 steps
-  c2     10M keys over a 256k vocabulary, length 4-12, Zipf(1.1); beam = K =
-         1000, 12 steps
+Workloads (--config):
+  paper   800M unique keys over a 2.2M-token vocabulary, key length 3-16
+          (mean ~6), Zipf(1.05) prefix sharing; beam = K = 1000, 16 steps
+  c2      10M keys over a 256k vocabulary, length 4-12, Zipf(1.1); beam =
+          K = 100, 12 steps
+  stress  200M keys, 2.2M-child root, length 16-32; beam = K = 1000, 32
+          steps, early exit, thresholds -4 / -20
+
+Proposal models (--models): "example", the shape of the reference's example
+generator (examples/make_example_data.py:119-145; one seeded key path per
+beam slot, forced tokens U(-2.2,-0.2), distractors U(-12,-4)); "literal",
+the configuration as stated: log-softmax of N(0, 2.5^2) logits over the
+2.2M vocabulary with 30% of the mass on one seeded key path.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config paper]
 """
 
 import argparse
+import hashlib
 import json
 import os
 import re
@@ -38,12 +54,17 @@ sys.path.insert(0, os.path.join(ROOT, "flash-trie_amd"))
 
 METRIC = "mean/p99 trie-search ms @800M keys, beam 1000; peak q/s over batch 1-8"
 HBM_PEAK_GBS = 8000.0
-PUBLISHED_PEAK_QPS = 1539.0  # A100, beam 1000, batch 8 (README.md:64)
+# the reference on an A100 (README.md:48-64): batch-1 mean / p99 ms and
+# peak q/s over batch 1-8, per beam width
+PUBLISHED = {1000: (1.91, 3.31, 1539.0), 500: (1.36, 2.04, 2571.0),
+             100: (0.56, 0.70, 5754.0)}
+
+import workloads as wl  # noqa: E402
 
 ALPHA = 5.0
 # per workload: token / sentence log-prob thresholds and early exit
-RULES = {"paper": (-10.0, -40.0, False), "c2": (-10.0, -40.0, False),
-         "stress": (-4.0, -20.0, True)}
+RULES = {k: (v[0], v[1], v[3]) for k, v in wl.RULES.items()}
+KERNEL_SRC = os.path.join(ROOT, "flash-trie_amd", "csrc", "tbs_kernel.hip")
 
 
 def log(*a):
@@ -53,109 +74,198 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=400,
-                   help="timed launches per batch size")
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=200,
+                   help="timed device-resident launches per batch size")
+    p.add_argument("--warmup", type=int, default=20,
+                   help="untimed device-resident launches per batch size")
     p.add_argument("--config", default="paper", choices=["c2", "paper", "stress"])
-    p.add_argument("--beam", type=int, default=1000)
-    p.add_argument("--pool", type=int, default=512,
-                   help="distinct requests staged in HBM")
+    p.add_argument("--beam", type=int, default=0, help="0: the workload's")
+    p.add_argument("--requests", type=int, default=13000,
+                   help="seeded requests per pass of the boundary protocol")
+    p.add_argument("--passes", type=int, default=2, help="measured passes")
+    p.add_argument("--models", default="example,literal")
     p.add_argument("--batches", default="1,2,4,8")
-    p.add_argument("--cpu-seconds", type=float, default=15.0)
-    p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--boundary", type=int, default=100,
-                   help="batch-1 requests timed through the C++ boundary")
     p.add_argument("--beam-sweep", default="100,500",
-                   help="other beam widths (K = beam) timed at batch 1 "
+                   help="other beam widths (K = beam) swept at the boundary "
                         "(paper workload; empty to skip)")
+    p.add_argument("--sweep-requests", type=int, default=4000,
+                   help="requests per pass for the other beam widths")
+    p.add_argument("--pool", type=int, default=512,
+                   help="requests staged in HBM for the device-resident runs")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-threads", type=int, default=16,
+                   help="cap on CPU-baseline threads (the box's CPU share)")
+    p.add_argument("--as-written", action="store_true",
+                   help="also time the oracle's as-written cost model on one "
+                        "request (minutes at the paper trie's 2.2M-child root)")
+    p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
 
+def kernel_hash():
+    with open(KERNEL_SRC, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def measured_traffic(cfg, batch):
-    """HBM bytes per launch of the search kernel at this batch size, as
-    measured by rocprofv3 FETCH_SIZE + WRITE_SIZE runs and scaled by the same
-    counters of a copy kernel of known size; read from the committed counter
-    summary (None when it holds no figure for this workload and batch)."""
+    """HBM bytes per launch of the search kernel at this batch size, from
+    rocprofv3 FETCH_SIZE + WRITE_SIZE runs scaled by the same counters of a
+    copy kernel of known size, as committed in the counter summary -- only
+    when that summary was recorded on this kernel source (its
+    kernel_source_sha256 line); None otherwise."""
     path = os.path.join(ROOT, "profiles", f"tbs_kernel_{cfg}_traffic.txt")
     if not os.path.exists(path):
         return None
-    pat = re.compile(r"^traffic_bytes_per_launch\[(\d+)\]\s*=\s*(\d+)")
-    for line in open(path):
-        m = pat.match(line.strip())
-        if m and int(m.group(1)) == batch:
-            return int(m.group(2))
+    text = open(path).read()
+    m = re.search(r"^kernel_source_sha256\s*=\s*([0-9a-f]+)", text, re.M)
+    if not m or m.group(1) != kernel_hash():
+        return None
+    pat = re.compile(r"^traffic_bytes_per_launch\[(\d+)\]\s*=\s*(\d+)", re.M)
+    for b, v in pat.findall(text):
+        if int(b) == batch:
+            return int(v)
     return None
 
 
-def build_workload(ft, cfg, beam):
+DESC = {"c2": "10M-key trie, 256k vocab, key length 4-12, Zipf(1.1)",
+        "paper": "800M unique keys, 2.2M vocab, key length 3-16 (mean ~6), "
+                 "Zipf(1.05) prefix sharing",
+        "stress": "stress: 200M-key trie, 2.2M vocab (heavy-fanout root), key "
+                  "length 16-32, Zipf(1.05) prefix sharing; early exit, "
+                  "thresholds -4 / -20"}
+BEAM = {"c2": 100, "paper": 1000, "stress": 1000}
+
+
+def build_workload(ft, cfg):
     t0 = time.time()
-    if cfg == "c2":
-        vocab, steps = 262144, 12
-        toks, offs = ft.synth_keys(10_000_000, vocab, 4, 12, 1.1, 0)
-        log(f"keys generated in {time.time() - t0:.1f}s")
-        trie = ft.Trie()
-        trie.build_arrays(toks, offs)
-        del toks, offs
-        desc = "10M-key trie, 256k vocab, key length 4-12, Zipf(1.1)"
-    elif cfg == "stress":
-        vocab, steps = 2_200_000, 32
-        trie = ft.Trie()
-        os.environ["FT_SYNTH_VERBOSE"] = "1"
-        ft.synth_paper_trie(trie, 200_000_000, vocab, 1.05, 1, lmin=16,
-                            lmax=32, p_end=0.25)
-        desc = ("stress: 200M-key trie, 2.2M vocab (heavy-fanout root), key "
-                "length 16-32, Zipf(1.05) prefix sharing; early exit, "
-                "thresholds -4 / -20")
-    else:
-        vocab, steps = 2_200_000, 16
-        trie = ft.Trie()
-        os.environ["FT_SYNTH_VERBOSE"] = "1"  # per-level progress on stderr
-        ft.synth_paper_trie(trie, 800_000_000, vocab, 1.05, 0)
-        desc = ("800M-key trie, 2.2M vocab, key length 3-16 (mean ~6), "
-                "Zipf(1.05) prefix sharing")
+    os.environ["FT_SYNTH_VERBOSE"] = "1"  # per-level progress on stderr
+    trie = wl.trie(ft, cfg)
     log(f"trie: {trie.num_keys()} keys, {trie.num_nodes()} nodes, "
         f"{trie.total_size() / 2**30:.2f} GiB image, {time.time() - t0:.1f}s")
-    return trie, vocab, steps, desc
+    return trie, wl.VOCAB[cfg], wl.STEPS[cfg], BEAM[cfg], DESC[cfg]
 
 
-def beam_sweep(ft, trie, vocab, T, widths, steps, warmup, rules, ot=None):
-    """Batch-1 kernel latency at other beam widths (K = beam, as many seed
-    paths), each over its own pool of seeded requests; spot-checked against
-    the oracle when it is given."""
+def make_requests(ft, trie, cfg, model, first, n, B):
+    """Seeded requests [first, first + n) at beam B (K = B)."""
+    return wl.requests(ft, trie, cfg, model, first, n, B)
+
+
+def pass_stats(call_ms, batch):
+    """Per-pass statistics averaged across passes (flashtrie_bench.py:
+    270-291): q/s = requests of a pass / the sum of its call times; mean
+    and p99 of the per-call milliseconds."""
+    qps = [batch * len(r) / (r.sum() * 1e-3) for r in call_ms]
+    return {"qps": float(np.mean(qps)),
+            "mean_ms": float(np.mean([r.mean() for r in call_ms])),
+            "p99_ms": float(np.mean([np.percentile(r, 99) for r in call_ms])),
+            "qps_passes": [round(x, 1) for x in qps]}
+
+
+def boundary_sweep(ft, trie, beams, ids, lp, batches, rules, passes, what):
     tok_thr, sent_thr, early = rules
-    out = {}
-    for B in widths:
-        P = 64
-        ids, lp = ft.synth_requests(trie, 1000 + B, P, vocab, T, B, B, 0.3, 2.5,
-                                    True, 0, model=1)
-        beams = np.full((P, T), B, dtype=np.uint32)
-        ft.stage(trie, beams, ids, lp, tok_thr, sent_thr, ALPHA, early)
-        ft.launch(trie, 0, 3)  # untimed separator launch for kernel traces
-        for i in range(warmup):
-            ft.launch(trie, i % P, 1)
-        ft.sync(trie)
-        for i in range(steps):
-            ft.launch(trie, i % P, 1)
-        ms = ft.launch_times(trie, min(steps, 1024))
-        res = {"mean": round(float(ms.mean()), 4),
-               "p99": round(float(np.percentile(ms, 99)), 4)}
-        if ot is not None:
-            for first in range(0, P):
-                ft.launch(trie, first, 1)
-            ft.sync(trie)
-            cnt, norms, lens, toks, _ = ft.fetch(trie)
-            bad = 0
-            for r in range(4):
-                s_, n_ = ot.tbs(beams[r], ids[r], lp[r], tok_thr, sent_thr,
-                                ALPHA, early)
-                c = int(cnt[r])
-                g = [toks[r, j, :lens[r, j]].tolist() for j in range(c)]
-                bad += int(g != s_ or not np.array_equal(norms[r, :c], n_))
-            res["parity"] = {"checked": 4, "mismatches": bad}
-        out[str(B)] = res
-        log(f"beam {B}: batch-1 kernel mean {res['mean']:.3f} ms p99 "
-            f"{res['p99']:.3f} ms")
-    return out
+    out, hashes = {}, {}
+    for b in batches:
+        n = len(beams) - len(beams) % b
+        cm, ps, cnt, hs = ft.bench_boundary(trie, beams[:n], ids[:n], lp[:n], b,
+                                            tok_thr, sent_thr, ALPHA, early, 1,
+                                            passes)
+        st = pass_stats(cm, b)
+        st["wall_qps"] = float(np.mean(n / ps))
+        out[b] = st
+        hashes[b] = (cnt, hs)
+        log(f"{what} batch {b}: {st['qps']:.0f} q/s at the boundary "
+            f"(passes {st['qps_passes']}), mean {st['mean_ms']:.3f} ms "
+            f"p99 {st['p99_ms']:.3f} ms per call")
+    # the same requests give the same results at every batch size
+    b0 = batches[0]
+    same = all(np.array_equal(hashes[b][1], hashes[b0][1][:len(hashes[b][1])])
+               for b in batches)
+    return out, hashes, same
+
+
+def harness_qps(ft, trie, beams, ids, lp, batch, rules, n):
+    """Requests/s of the Python path the reference's harness times: lists
+    built per batch, then bs_tbs_gpu (examples/run_trie_search.py:189-199)."""
+    tok_thr, sent_thr, early = rules
+    n -= n % batch
+    t0 = time.perf_counter()
+    for b0 in range(0, n, batch):
+        ft.bs_tbs_gpu(trie, batch, beams[b0:b0 + batch].tolist(),
+                      ids[b0:b0 + batch].tolist(), lp[b0:b0 + batch].tolist(),
+                      tok_thr, sent_thr, ALPHA, early)
+    return n / (time.perf_counter() - t0)
+
+
+def fnv_results(sents, norms):
+    """The hash bench_boundary computes over one request's results."""
+    h = 0xcbf29ce484222325
+    m = (1 << 64) - 1
+
+    def mix(w):
+        nonlocal h
+        h = ((h ^ w) * 0x100000001b3) & m
+    mix(len(sents))
+    bits = np.asarray(norms, dtype=np.float64).view(np.uint64)
+    for s, nb in zip(sents, bits):
+        mix(len(s))
+        for tk in s:
+            mix(int(tk))
+        nb = int(nb)
+        mix(nb & 0xFFFFFFFF)
+        mix(nb >> 32)
+    return h
+
+
+def oracle_of(trie):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    return pyoracle, wl.oracle(pyoracle, trie)
+
+
+def cpu_info():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, aff
+
+
+def run_oracle(ot, reqs, rules, seconds, threads, with_work=False):
+    """Runs the oracle over reqs (list of (beams, ids, lp)) on `threads`
+    host threads until done or `seconds` pass; returns ({index: (sents,
+    norms)}, works, elapsed seconds)."""
+    tok_thr, sent_thr, early = rules
+    done, works, lock, nxt = {}, [], threading.Lock(), [0]
+    deadline = time.time() + seconds
+
+    def worker():
+        while time.time() < deadline:
+            with lock:
+                r = nxt[0]
+                nxt[0] += 1
+            if r >= len(reqs):
+                return
+            bm, i_, l_ = reqs[r]
+            res = ot.tbs(bm, i_, l_, tok_thr, sent_thr, ALPHA, early,
+                         with_work=with_work)
+            with lock:
+                done[r] = res[:2]
+                if with_work:
+                    works.append(res[2])
+
+    t0 = time.time()
+    th = [threading.Thread(target=worker) for _ in range(threads)]
+    [x.start() for x in th]
+    [x.join() for x in th]
+    return done, works, time.time() - t0
 
 
 def main():
@@ -171,68 +281,77 @@ def main():
         ftbuild.build()
     import flashtrie as ft
 
-    B = K = args.beam
-    TOK_THR, SENT_THR, EARLY = RULES[args.config]
-    trie, vocab, T, desc = build_workload(ft, args.config, B)
+    rules = RULES[args.config]
+    trie, vocab, T, beam0, desc = build_workload(ft, args.config)
+    B = args.beam or beam0
     batches = [int(x) for x in args.batches.split(",")]
-    P = args.pool
+    models = [m for m in args.models.split(",") if m]
+    widths = [int(x) for x in args.beam_sweep.split(",") if x.strip()]
+    widths = [w for w in widths if w < B] if args.config == "paper" else []
     t0 = time.time()
-    ids, lp = ft.synth_requests(trie, 0, P, vocab, T, K, B, 0.3, 2.5, True, 0,
-                                model=1)
-    beams = np.full((P, T), B, dtype=np.uint32)
-    log(f"{P} requests generated in {time.time() - t0:.1f}s")
-
-    trie.init_tbs_gpu(max(batches), max_num_topk=K, max_num_outpos=T,
+    trie.init_tbs_gpu(max(batches), max_num_topk=B, max_num_outpos=T,
                       max_num_out_beams=B, max_num_out_tokens=B * T,
                       max_num_inter_beams=B * T)
-    ft.reserve_staging(trie, P)
     info = trie.device_info()
-    log("device", info)
-    ft.stage(trie, beams, ids, lp, TOK_THR, SENT_THR, ALPHA, EARLY)
+    log(f"device {info}; context ready in {time.time() - t0:.1f}s")
+
+    # ---- the boundary protocol, per proposal model ------------------------
+    boundary, reqsets, hashsets = {}, {}, {}
+    for model in models:
+        t0 = time.time()
+        beams, ids, lp = make_requests(ft, trie, args.config, model, 0, args.requests, B)
+        log(f"{model}: {args.requests} requests generated in {time.time() - t0:.1f}s")
+        sweep, hashes, same = boundary_sweep(ft, trie, beams, ids, lp, batches,
+                                             rules, args.passes, f"{model} beam {B}")
+        hq = harness_qps(ft, trie, beams, ids, lp, max(batches), rules,
+                         min(1024, args.requests))
+        log(f"{model}: harness wall {hq:.0f} q/s at batch {max(batches)}")
+        boundary[model] = {B: {"by_batch": sweep, "harness_qps": hq,
+                               "same_results_every_batch": same}}
+        reqsets[model] = (beams, ids, lp)
+        hashsets[model] = hashes
+    head = models[0]
+    head_sweep = boundary[head][B]["by_batch"]
+    peak_b = max(head_sweep, key=lambda b: head_sweep[b]["qps"])
+
+    # ---- device-resident runs (kernel-only extras) -------------------------
+    beams, ids, lp = reqsets[head]
+    P = min(args.pool, args.requests)
+    ft.reserve_staging(trie, P)
+    ft.stage(trie, beams[:P], ids[:P], lp[:P], *rules[:2], ALPHA, rules[2])
     ft.launch(trie, 0, 1)
     ft.sync(trie)
-
-    # ---- device-resident throughput and latency per batch size ----------
-    qps, kern_ms, results = {}, {}, {}
+    dev_qps, kern_ms = {}, {}
     for b in batches:
         nb = P // b
-        # one untimed batch-3 launch before each batch size: its grid size
-        # differs from every timed one, so a kernel trace splits into one run
-        # of dispatches per batch size (and from the first launch above)
+        # an untimed batch-3 launch before each batch size splits a kernel
+        # trace into one run of dispatches per batch size
         ft.launch(trie, 0, min(3, P))
         for i in range(args.warmup):
             ft.launch(trie, (i % nb) * b, b)
         ft.sync(trie)
-        t0 = time.perf_counter()
+        t1 = time.perf_counter()
         for i in range(args.steps):
             ft.launch(trie, (i % nb) * b, b)
         ft.sync(trie)
-        el = time.perf_counter() - t0
-        n = min(args.steps, 1024)
-        ms = ft.launch_times(trie, n)
-        qps[b] = args.steps * b / el
-        kern_ms[b] = ms
-        log(f"batch {b}: {qps[b]:.0f} q/s, kernel mean {ms.mean():.3f} ms "
-            f"p99 {np.percentile(ms, 99):.3f} ms")
-    peak_b = max(qps, key=qps.get)
-
-    # results + per-phase device time of the whole pool (batches of max b)
+        el = time.perf_counter() - t1
+        dev_qps[b] = args.steps * b / el
+        kern_ms[b] = ft.launch_times(trie, min(args.steps, 1024))
+        log(f"device-resident batch {b}: {dev_qps[b]:.0f} q/s, kernel mean "
+            f"{kern_ms[b].mean():.3f} ms p99 {np.percentile(kern_ms[b], 99):.3f} ms")
+    dev_peak = max(dev_qps, key=dev_qps.get)
     mb = max(batches)
-    counts, lens_all, phase = [], [], []
-    sample_out = {}
-    for first in range(0, P - P % mb, mb):
+    used = P - P % mb
+    for first in range(0, used, mb):
         ft.launch(trie, first, mb)
+    if used < P:
+        ft.launch(trie, used, P - used)
     ft.sync(trie)
     cnt, norms, lens, toks, timing = ft.fetch(trie)
-    used = P - P % mb
-    counts = cnt[:used]
-    dev = timing["device_ms"][:used]
-    phase = {"expand_ms": float(dev[:, 0].mean()),
-             "select_ms": float(dev[:, 1].mean()),
-             "other_ms": float(dev[:, 2].mean()),
-             "device_total_ms": float(dev[:, 3].mean())}
-
-    ss = timing["step_stats"][:used].astype(np.float64)
+    dev = timing["device_ms"]
+    phase = {"expand_ms": float(dev[:, 0].mean()), "select_ms": float(dev[:, 1].mean()),
+             "other_ms": float(dev[:, 2].mean()), "device_total_ms": float(dev[:, 3].mean())}
+    ss = timing["step_stats"].astype(np.float64)
     tick_ms = 1.0 / info["wall_clock_khz"]
     log("per step (mean over the pool): parents, work, next, sel, expand_ms, "
         "select_ms, children, probes")
@@ -240,168 +359,158 @@ def main():
         m = ss[:, t, :].mean(axis=0)
         log(f"  step {t:2d}: {m[0]:7.1f} {m[1]:9.1f} {m[2]:7.1f} {m[3]:6.1f} "
             f"{m[4] * tick_ms:7.4f} {m[5] * tick_ms:7.4f} {m[6]:9.1f} {m[7]:9.1f}")
-    log(f"phases per request (ms): {phase}; kernel counters: "
-        f"{ {k: timing[k] for k in ('candidates', 'parents', 'children', 'probes')} }")
-    # ---- batch-1 latency through the C++ boundary (host arrays) -----------
-    bl = []
-    nbd = min(args.boundary, P)
-    ft.launch(trie, 0, min(3, P))  # untimed separator launch for kernel traces
-    ft.sync(trie)
-    for r in range(nbd):
-        t0 = time.perf_counter()
-        ft.stage(trie, beams[r:r + 1], ids[r:r + 1], lp[r:r + 1], TOK_THR,
-                 SENT_THR, ALPHA, EARLY)
-        ft.launch(trie)
-        c1, n1, l1, t1, _ = ft.fetch(trie)
-        bl.append((time.perf_counter() - t0) * 1e3)
-    bl = np.array(bl)
-    if bl.size:
-        log(f"boundary latency: mean {bl.mean():.3f} ms p99 "
-            f"{np.percentile(bl, 99):.3f} ms")
 
-    # ---- CPU oracle baseline on a bounded sample + parity spot check -------
-    cpu = None
-    parity = {"checked": 0, "mismatches": 0}
-    algo_bytes = None
+    # ---- other beam widths at the boundary ----------------------------------
+    for w in widths:
+        for model in models:
+            bw, iw, lw = make_requests(ft, trie, args.config, model, 100000 * w,
+                                       args.sweep_requests, w)
+            sweep, _, same = boundary_sweep(ft, trie, bw, iw, lw, batches, rules,
+                                            args.passes, f"{model} beam {w}")
+            boundary[model][w] = {"by_batch": sweep, "same_results_every_batch": same}
+            reqsets[(model, w)] = (bw, iw, lw)
+
+    # ---- CPU oracle: baseline on a bounded sample, parity, work counters ----
+    cpu, parity, algo_bytes, wstats = None, {}, None, {}
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import pyoracle
-        img = trie.image_view()
-        hdr = np.frombuffer(img[:64].tobytes(), dtype="<u8", count=8)
-        nn, ro, to, tl = int(hdr[1]), int(hdr[4]), int(hdr[6]), int(hdr[3])
-        recs = img[ro:ro + (nn + 1) * 16]
-        tail = img[to:to + max(tl, 1) * 4].view(np.uint32)
-        ot = pyoracle.OracleTrie.from_image(recs, tail, nn)
-        cores = min(os.cpu_count() or 1, 16)
-        done, works, lock = [], [], threading.Lock()
-        deadline = time.time() + args.cpu_seconds
-        nxt = [0]
-
-        def worker():
-            while time.time() < deadline:
-                with lock:
-                    r = nxt[0]
-                    nxt[0] += 1
-                if r >= P:
-                    return
-                s, n, w = ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR,
-                                 ALPHA, EARLY, with_work=True)
-                with lock:
-                    done.append((r, s, n))
-                    works.append(w)
-
-        t0 = time.time()
-        log(f"cpu baseline: {cores} threads for {args.cpu_seconds:.0f}s")
-        th = [threading.Thread(target=worker) for _ in range(cores)]
-        [x.start() for x in th]
-        [x.join() for x in th]
-        cpu_el = time.time() - t0
-        # single-thread latency of the same restatement, and the as-written
-        # cost model (thread per parent, linear sibling scan) on 2 requests
+        pyoracle, ot = oracle_of(trie)
+        model_name, nproc, aff = cpu_info()
+        threads = max(1, min(args.cpu_threads, aff))
+        hb, hi, hl = reqsets[head]
+        sample = [(hb[r], hi[r], hl[r]) for r in range(args.requests)]
+        log(f"cpu baseline: {threads} threads for {args.cpu_seconds:.0f}s")
+        done, works, cpu_el = run_oracle(ot, sample, rules, args.cpu_seconds,
+                                         threads, with_work=True)
         lat1 = []
         for r in range(3):
             t1 = time.perf_counter()
-            ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, EARLY)
+            ot.tbs(hb[r], hi[r], hl[r], *rules[:2], ALPHA, rules[2])
             lat1.append((time.perf_counter() - t1) * 1e3)
-        # the as-written linear sibling scan costs O(K x degree) per parent:
-        # ~2e9 label reads at the 2.2M-child root of the paper trie, so it
-        # is timed on the smaller trie only
-        aw = []
-        if args.config == "c2":
-            for r in range(2):
-                t1 = time.perf_counter()
-                ot.tbs(beams[r], ids[r], lp[r], TOK_THR, SENT_THR, ALPHA, EARLY,
-                       variant=pyoracle.AS_WRITTEN)
-                aw.append((time.perf_counter() - t1) * 1e3)
-        aw_txt = (f"{np.mean(aw):.1f} ms/request" if aw else
-                  "not run (O(K x root degree) = ~2e9 label reads at step 0)")
-        cpu = {"value": len(done) / cpu_el, "unit": "q/s", "cores": cores,
+        aw_txt = "not run (--as-written times it)"
+        if args.as_written:
+            t1 = time.perf_counter()
+            ot.tbs(hb[0], hi[0], hl[0], *rules[:2], ALPHA, rules[2],
+                   variant=pyoracle.AS_WRITTEN)
+            aw_txt = f"{(time.perf_counter() - t1) * 1e3:.0f} ms for request 0"
+        cpu = {"value": len(done) / cpu_el, "unit": "q/s", "cores": threads,
                "kind": "port",
-               "sample": f"{len(done)} of the {P} pooled requests in "
-                         f"{cpu_el:.1f}s on {cores} threads (oracle, binary "
-                         f"sibling search); 1-thread latency "
-                         f"{np.mean(lat1):.1f} ms; as-written cost model "
-                         f"(thread per parent, linear sibling scan) "
-                         f"{aw_txt}"}
-        # parity of the GPU results for the sampled requests
-        for r, s, n in done:
-            if r >= used:
+               "sample": f"{len(done)} of the {args.requests} {head}-model "
+                         f"requests at beam {B} in {cpu_el:.1f}s on {threads} "
+                         f"threads (oracle, binary sibling search, one thread "
+                         f"per request); 1-thread latency {np.mean(lat1):.1f} ms; "
+                         f"as-written cost model (thread per parent, linear "
+                         f"sibling scan): {aw_txt}",
+               "host": {"cpu_model": model_name, "nproc": nproc,
+                        "affinity_cpus": aff, "thread_cap": args.cpu_threads,
+                        "pinning": "none (the process's affinity mask)"}}
+        # parity: every sampled request's boundary results (last pass, at
+        # every batch size) against the oracle's
+        for model in models:
+            mb_, mi, ml = reqsets[model]
+            if model == head:
+                chk = done
+            else:
+                chk, _, _ = run_oracle(ot, [(mb_[r], mi[r], ml[r]) for r in range(512)],
+                                       rules, args.cpu_seconds, threads)
+            bad = 0
+            for r, (s_, n_) in chk.items():
+                hv = fnv_results(s_, n_)
+                for b, (cn, hs) in hashsets[model].items():
+                    if r < len(hs) and (int(hs[r]) != hv or int(cn[r]) != len(s_)):
+                        bad += 1
+                        break
+            parity[model] = {"checked": len(chk), "mismatches": bad,
+                             "batches": batches}
+            log(f"parity {model}: {len(chk)} requests, {bad} mismatches")
+        for (model, w), (bw, iw, lw) in [(k, v) for k, v in reqsets.items()
+                                         if isinstance(k, tuple)]:
+            chk, _, _ = run_oracle(ot, [(bw[r], iw[r], lw[r]) for r in range(16)],
+                                   rules, args.cpu_seconds, threads)
+            sweep_hash = ft.bench_boundary(trie, bw[:16], iw[:16], lw[:16], 1,
+                                           *rules[:2], ALPHA, rules[2], 0, 1)
+            bad = sum(int(sweep_hash[3][r]) != fnv_results(*chk[r]) for r in chk)
+            boundary[model][w]["parity"] = {"checked": len(chk), "mismatches": bad}
+        # device-resident results of the pool against the oracle
+        bad = 0
+        for r, (s_, n_) in done.items():
+            if r >= P:
                 continue
-            c = int(counts[r])
+            c = int(cnt[r])
             g = [toks[r, j, :lens[r, j]].tolist() for j in range(c)]
-            parity["checked"] += 1
-            if g != s or not np.array_equal(norms[r, :c], n):
-                parity["mismatches"] += 1
-        # algorithmic bytes per request (work counters of the oracle):
-        # 8K per row + 16 per parent + 16 per non-link parent + 4 per child
-        # label touched + 32 per candidate + 16 per survivor + result bytes
+            bad += int(g != s_ or not np.array_equal(norms[r, :c], n_))
+        parity["device_resident"] = {"checked": sum(r < P for r in done),
+                                     "mismatches": bad}
+        # algorithmic bytes per request (oracle work counters): 8K per row +
+        # 16 per parent + 16 per non-link parent + 4 per child label touched
+        # + 32 per candidate + 16 per survivor + result bytes
         W = np.array(works, dtype=np.float64)
         res_b = np.array([16 + 16 * len(s) + 4 * sum(map(len, s))
-                          for _, s, _ in done], dtype=np.float64)
+                          for s, _ in done.values()], dtype=np.float64)
         per_req = (W[:, 6] + 16 * W[:, 1] + 16 * (W[:, 1] - W[:, 2]) +
                    4 * W[:, 3] + 32 * W[:, 4] + 16 * W[:, 5] + res_b)
         algo_bytes = float(per_req.mean())
         wstats = {"steps": float(W[:, 0].mean()), "parents": float(W[:, 1].mean()),
                   "link_parents": float(W[:, 2].mean()),
                   "candidates": float(W[:, 4].mean()),
-                  "results": float(np.mean([len(s) for _, s, _ in done]))}
-    else:
-        wstats = {}
+                  "results": float(np.mean([len(s) for s, _ in done.values()]))}
 
-    # ---- other beam widths at batch 1 (after everything that reads the
-    # staged pool) ------------------------------------------------------------
-    by_beam = {}
-    widths = [int(x) for x in args.beam_sweep.split(",") if x.strip()]
-    if args.config == "paper" and widths:
-        by_beam = beam_sweep(ft, trie, vocab, T, [w for w in widths if w <= B],
-                             min(args.steps, 300), args.warmup,
-                             RULES[args.config], None if args.no_cpu else ot)
-
-    kb = kern_ms[peak_b]
+    kb = kern_ms[dev_peak]
     roof = None
     if algo_bytes is not None:
-        achieved = algo_bytes * peak_b / (kb.mean() * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 3),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS,
-                "traffic": measured_traffic(args.config, peak_b),
+        achieved = algo_bytes * dev_peak / (kb.mean() * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                "traffic": measured_traffic(args.config, dev_peak),
                 "algorithmic_bytes_per_request": round(algo_bytes),
-                "requests_per_launch": peak_b}
-    k1 = kern_ms.get(1, kb)
+                "requests_per_launch": dev_peak,
+                "launch_ms": round(float(kb.mean()), 4),
+                "kernel_source_sha256": kernel_hash()}
+
+    hp = head_sweep[peak_b]
+    l1 = head_sweep.get(1, hp)
+    calls_peak = args.requests // peak_b
+    pub = PUBLISHED.get(B) if args.config == "paper" else None
+
+    def fmt_sweep(sw):
+        return {str(b): {"qps": round(v["qps"], 1), "mean_ms": round(v["mean_ms"], 4),
+                         "p99_ms": round(v["p99_ms"], 4),
+                         "wall_qps": round(v["wall_qps"], 1)} for b, v in sw.items()}
+
     out = {
         "metric": METRIC,
-        "value": round(qps[peak_b], 1),
+        "value": round(hp["qps"], 1),
         "unit": "q/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(float(kb.mean()), 4),
+        "steps": calls_peak * args.passes,
+        "warmup": calls_peak,
+        "ms_per_step": round(hp["mean_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (round(qps[peak_b] / PUBLISHED_PEAK_QPS, 3)
-                        if args.config == "paper" else None),
+        "vs_baseline": round(hp["qps"] / pub[2], 3) if pub else None,
         "dtype": "f64",
         "data": "synthetic",
-        "config": {"workload": desc, "beam": B, "topk": K, "steps": T,
+        "config": {"workload": desc, "beam": B, "topk": B, "steps": T,
                    "batch_sizes": batches, "peak_batch": peak_b,
-                   "requests_pooled": P,
-                   "proposals": "example row model: seed-path tokens "
-                                "U(-2.2,-0.2), distractors U(-12,-4), "
-                                f"{B} seed paths",
-                   "thresholds": [TOK_THR, SENT_THR], "length_norm": ALPHA,
-                   "early_exit": EARLY},
-        "latency_ms": {"mean": round(float(k1.mean()), 4),
-                       "p99": round(float(np.percentile(k1, 99)), 4),
-                       "boundary_mean": (round(float(bl.mean()), 4)
-                                         if bl.size else None),
-                       "boundary_p99": (round(float(np.percentile(bl, 99)), 4)
-                                        if bl.size else None)},
-        "latency_ms_by_beam": dict(
-            by_beam, **{str(B): {"mean": round(float(kern_ms.get(1, kb).mean()), 4),
-                                 "p99": round(float(np.percentile(kern_ms.get(1, kb), 99)), 4)}}),
-        "qps_by_batch": {str(b): round(v, 1) for b, v in qps.items()},
-        "kernel_ms_by_batch": {str(b): round(float(v.mean()), 4)
-                               for b, v in kern_ms.items()},
+                   "requests_per_pass": args.requests, "passes": args.passes,
+                   "warmup_passes": 1, "headline_model": head,
+                   "models": models,
+                   "boundary": "C++ wall time around Trie::tbs_gpu_batched "
+                               "(tools/bindings.cpp:90-100): staging, H2D, "
+                               "kernel, D2H, output vectors",
+                   "thresholds": list(rules[:2]), "length_norm": ALPHA,
+                   "early_exit": rules[2]},
+        "latency_ms": {"mean": round(l1["mean_ms"], 4), "p99": round(l1["p99_ms"], 4),
+                       "kernel_mean": round(float(kern_ms.get(1, kb).mean()), 4),
+                       "kernel_p99": round(float(np.percentile(kern_ms.get(1, kb), 99)), 4)},
+        "boundary": {m: {str(w): dict(v, by_batch=fmt_sweep(v["by_batch"]))
+                         for w, v in d.items()} for m, d in boundary.items()},
+        "published_a100": ({str(k): {"mean_ms": v[0], "p99_ms": v[1], "peak_qps": v[2]}
+                            for k, v in PUBLISHED.items()} if args.config == "paper"
+                           else None),
+        "device_resident": {"qps_by_batch": {str(b): round(v, 1) for b, v in dev_qps.items()},
+                            "kernel_ms_by_batch": {str(b): round(float(v.mean()), 4)
+                                                   for b, v in kern_ms.items()},
+                            "requests_pooled": P, "launches": args.steps},
         "phases_ms_per_request": phase,
         "workload_stats": wstats,
         "parity": parity,

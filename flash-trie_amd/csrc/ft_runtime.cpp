@@ -8,6 +8,8 @@
 // tbs-kernels.cu:686-700).
 #include <hip/hip_runtime.h>
 
+#include <emmintrin.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -691,11 +693,142 @@ struct StageLimits {
   uint64_t max_steps, max_topk, max_out_beams, max_out_tokens;
 };
 
+// One proposal row: whether it holds NaN or +inf, whether its token ids are
+// strictly ascending, and the least and greatest logp above the token
+// threshold (+inf / -inf when none is); the row is copied to oid / olp on
+// the way.  One branch-free SSE2 pass, four proposals at a time.
+struct RowScan {
+  bool bad, sorted;
+  float lo, hi;
+};
+static RowScan scan_row(const uint32_t* rid, const float* rlp, uint32_t K, float thr,
+                        uint32_t* oid, float* olp) {
+  const __m128 vinf = _mm_set1_ps(INFINITY), vninf = _mm_set1_ps(-INFINITY);
+  const __m128 vthr = _mm_set1_ps(thr);
+  const __m128i flip = _mm_set1_epi32((int)0x80000000u), ones = _mm_set1_epi32(-1);
+  bool bad = false, sorted = true;
+  float lo = INFINITY, hi = -INFINITY;
+  uint32_t k = 1;
+  if (K >= 5) {
+    __m128 vlo = vinf, vhi = vninf, vbad = _mm_setzero_ps();
+    __m128i vuns = _mm_setzero_si128();
+    for (; k + 4 <= K; k += 4) {
+      const __m128 x = _mm_loadu_ps(rlp + k);
+      _mm_storeu_ps(olp + k, x);
+      vbad = _mm_or_ps(vbad, _mm_or_ps(_mm_cmpunord_ps(x, x), _mm_cmpeq_ps(x, vinf)));
+      const __m128 keep = _mm_cmpgt_ps(x, vthr);
+      vlo = _mm_min_ps(vlo, _mm_or_ps(_mm_and_ps(keep, x), _mm_andnot_ps(keep, vinf)));
+      vhi = _mm_max_ps(vhi, _mm_or_ps(_mm_and_ps(keep, x), _mm_andnot_ps(keep, vninf)));
+      // unsigned rid[i] > rid[i - 1] as a signed compare of flipped words
+      const __m128i ra = _mm_loadu_si128((const __m128i*)(rid + k));
+      _mm_storeu_si128((__m128i*)(oid + k), ra);
+      const __m128i a = _mm_xor_si128(ra, flip);
+      const __m128i b = _mm_xor_si128(_mm_loadu_si128((const __m128i*)(rid + k - 1)), flip);
+      vuns = _mm_or_si128(vuns, _mm_xor_si128(_mm_cmpgt_epi32(a, b), ones));
+    }
+    alignas(16) float l4[4], h4[4];
+    alignas(16) uint32_t b4[4], u4[4];
+    _mm_store_ps(l4, vlo);
+    _mm_store_ps(h4, vhi);
+    _mm_store_si128((__m128i*)b4, _mm_castps_si128(vbad));
+    _mm_store_si128((__m128i*)u4, vuns);
+    for (int j = 0; j < 4; ++j) {
+      lo = std::min(lo, l4[j]);
+      hi = std::max(hi, h4[j]);
+      bad = bad || b4[j] != 0;
+      sorted = sorted && u4[j] == 0;
+    }
+  }
+  auto one = [&](uint32_t i) {
+    const float x = rlp[i];
+    olp[i] = x;
+    oid[i] = rid[i];
+    bad = bad || std::isnan(x) || x == INFINITY;
+    if (x > thr) {
+      lo = std::min(lo, x);
+      hi = std::max(hi, x);
+    }
+    if (i > 0 && rid[i] <= rid[i - 1]) sorted = false;
+  };
+  if (K) one(0);
+  for (; k < K; ++k) one(k);
+  return RowScan{bad, sorted, lo, hi};
+}
+
+// Packs one validated request into its block at `base` (see pack_batch):
+// the length-norm table, beam widths, token-sorted rows and per-step key
+// bounds.  Fails on NaN / +inf logps, duplicate token ids in a row and
+// non-finite length-norm factors.  `tmp` holds K pairs.
+static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
+                        std::pair<uint32_t, uint32_t>* tmp, std::string* err) {
+  auto who = [r]() { return "request " + std::to_string(r) + ": "; };
+  const uint32_t T = d.T, K = d.K;
+  // length-norm table, exactly Agent::logp_norm's factor (agent.h:69-72)
+  double* lnf = (double*)base;
+  // (depth 0 is the root alone, whose norm is never compared)
+  for (uint32_t dd = 0; dd <= T; ++dd) {
+    lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
+    if (dd > 0 && !std::isfinite(lnf[dd]))
+      return *err = who() + "length_norm gives a non-finite factor", FT_E_INPUT;
+  }
+  std::memcpy(base + d.beams_off, q.beams, 4ull * T);
+  uint32_t* rid_s = (uint32_t*)(base + d.rid_off);
+  float* rlp_s = (float*)(base + d.rlp_off);
+  uint16_t* rk_s = (uint16_t*)(base + d.rk_off);
+  uint64_t* kb = (uint64_t*)(base + d.kb_off);
+  // Per step, bounds of the keys pushed into `next`: a push's score is a
+  // parent score plus a logp that passes the token threshold, and itself
+  // passes the sentence threshold; parent scores are bounded by the same
+  // recursion one step earlier.  Double additions and the multiplication
+  // by the length factor are monotone, so the bounds hold exactly for the
+  // device's arithmetic (which this repeats).  A row with no logp above
+  // the threshold contributes 0 to both bounds (it pushes nothing).
+  double s_lo = 0.0, s_hi = 0.0;  // parent scores at step t
+  for (uint32_t t = 0; t < T; ++t) {
+    const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
+    const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
+    if (!rid || !rlp) return *err = who() + "null topk row", FT_E_ARG;
+    // rows in ascending token order, with each proposal's index in the
+    // caller's row (the order the reference visits proposals in)
+    uint32_t* oid = rid_s + (uint64_t)t * K;
+    float* olp = rlp_s + (uint64_t)t * K;
+    uint16_t* ok = rk_s + (uint64_t)t * K;
+    const RowScan sc = scan_row(rid, rlp, K, q.token_logp_threshold, oid, olp);
+    if (sc.bad) return *err = who() + "topk_logp holds NaN or +inf", FT_E_INPUT;
+    if (sc.sorted) {
+      for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
+    } else {
+      for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
+      std::sort(tmp, tmp + K);
+      for (uint32_t p = 0; p < K; ++p) {
+        if (p && tmp[p].first == tmp[p - 1].first)
+          return *err = who() + "duplicate token id " + std::to_string(tmp[p].first) +
+                        " in topk row " + std::to_string(t),
+                 FT_E_INPUT;
+        oid[p] = tmp[p].first;
+        olp[p] = rlp[tmp[p].second];
+        ok[p] = (uint16_t)tmp[p].second;
+      }
+    }
+    const bool any = sc.hi >= sc.lo;
+    const double x_lo = any ? (double)sc.lo : 0.0, x_hi = any ? (double)sc.hi : 0.0;
+    const double lo = std::max(q.sent_logp_threshold, s_lo + x_lo);
+    const double hi = s_hi + x_hi;
+    kb[2 * t] = host_norm_key(lo * lnf[t + 1]);
+    kb[2 * t + 1] = host_norm_key(hi * lnf[t + 1]);
+    s_lo = lo;
+    s_hi = hi;
+  }
+  return FT_OK;
+}
+
 // Validates `batch` requests and packs them into H (cap bytes): DevReq[batch]
 // then each request's block (length-norm table, beam widths, token-sorted
 // rows, key bounds).  Fills staged[0, batch); *bytes = bytes used,
-// *out_stride = output bytes per request.  `tmp` holds max_topk pairs
-// (sorting an unsorted row).  Allocates nothing on success.
+// *out_stride = output bytes per request.  `tmp` holds max_topk pairs (the
+// buffer an unsorted row is sorted in).
+// An error names the first request (in batch order) that has one.
+// Allocates nothing on success.
 static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& lim,
                       uint8_t* H, uint64_t cap, StagedReq* staged,
                       std::pair<uint32_t, uint32_t>* tmp, uint64_t* bytes,
@@ -703,13 +836,23 @@ static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& l
   DevReq* D = (DevReq*)H;
   uint64_t off = align_up(batch * sizeof(DevReq), 256);
   uint64_t max_out = sizeof(OutHeader);
-  for (size_t r = 0; r < batch; ++r) {
+  size_t first_bad = batch;
+  int first_rc = FT_OK;
+  std::string first_msg;
+  for (size_t r = 0; r < batch && first_bad == batch; ++r) {
     const ft_request& q = reqs[r];
     auto who = [r]() { return "request " + std::to_string(r) + ": "; };
+    auto bad = [&](int rc, const std::string& m) {
+      first_bad = r;
+      first_rc = rc;
+      first_msg = m;
+    };
     DevReq d{};
     StagedReq& st = staged[r];
-    if (q.num_beams == 0 || !q.beams)
-      return fail(FT_E_INPUT, who() + "beams is empty");
+    if (q.num_beams == 0 || !q.beams) {
+      bad(FT_E_INPUT, who() + "beams is empty");
+      break;
+    }
     const uint32_t F = q.beams[q.num_beams - 1];
     if (F == 0) {  // outputs untouched (louds-trie.cc:114-117)
       st.skip = true;
@@ -719,37 +862,68 @@ static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& l
       continue;
     }
     const uint32_t T = q.num_steps, K = q.topk;
-    if (T == 0 || K == 0)
-      return fail(FT_E_INPUT, who() + "topk rows are empty");
-    if (q.num_beams < T)
-      return fail(FT_E_INPUT, who() + "fewer beam widths than topk rows");
-    if (T > lim.max_steps)
-      return fail(FT_E_LIMIT, who() + "steps " + std::to_string(T) +
-                                  " > max_num_outpos " + std::to_string(lim.max_steps));
-    if (K > lim.max_topk)
-      return fail(FT_E_LIMIT, who() + "topk " + std::to_string(K) +
-                                  " > max_num_topk " + std::to_string(lim.max_topk));
-    if (F > lim.max_out_beams)
-      return fail(FT_E_LIMIT, who() + "final beam > max_num_out_beams");
-    if ((uint64_t)F * T > lim.max_out_tokens)
-      return fail(FT_E_LIMIT, who() + "final beam * steps > max_num_out_tokens");
-    for (uint32_t t = 0; t < T; ++t) {
-      if (q.beams[t] == 0)
-        return fail(FT_E_INPUT, who() + "beam width 0 at step " + std::to_string(t));
-      if (q.beams[t] > lim.max_out_beams)
-        return fail(FT_E_LIMIT, who() + "beam width > max_num_out_beams");
+    if (T == 0 || K == 0) {
+      bad(FT_E_INPUT, who() + "topk rows are empty");
+      break;
     }
-    if (!q.topk_id_rows && (!q.topk_id || !q.topk_logp))
-      return fail(FT_E_ARG, who() + "null topk arrays");
-    if (q.topk_id_rows && !q.topk_logp_rows)
-      return fail(FT_E_ARG, who() + "null topk_logp rows");
-    // the request's block must fit before anything is written
-    const uint64_t need = align_up(8ull * (T + 1), 16) + align_up(4ull * T, 16) +
-                          2 * align_up(4ull * T * K, 16) + align_up(2ull * T * K, 16) +
-                          align_up(16ull * T, 16);
-    if (off + need > cap)
-      return fail(FT_E_LIMIT, who() + "the staged batch exceeds the staging buffer (" +
-                                  std::to_string(cap) + " bytes)");
+    if (q.num_beams < T) {
+      bad(FT_E_INPUT, who() + "fewer beam widths than topk rows");
+      break;
+    }
+    if (T > lim.max_steps) {
+      bad(FT_E_LIMIT, who() + "steps " + std::to_string(T) + " > max_num_outpos " +
+                          std::to_string(lim.max_steps));
+      break;
+    }
+    if (K > lim.max_topk) {
+      bad(FT_E_LIMIT, who() + "topk " + std::to_string(K) + " > max_num_topk " +
+                          std::to_string(lim.max_topk));
+      break;
+    }
+    if (F > lim.max_out_beams) {
+      bad(FT_E_LIMIT, who() + "final beam > max_num_out_beams");
+      break;
+    }
+    if ((uint64_t)F * T > lim.max_out_tokens) {
+      bad(FT_E_LIMIT, who() + "final beam * steps > max_num_out_tokens");
+      break;
+    }
+    uint64_t bmax = F, hsum = 0;
+    for (uint32_t t = 0; t < T && first_bad == batch; ++t) {
+      if (q.beams[t] == 0)
+        bad(FT_E_INPUT, who() + "beam width 0 at step " + std::to_string(t));
+      else if (q.beams[t] > lim.max_out_beams)
+        bad(FT_E_LIMIT, who() + "beam width > max_num_out_beams");
+      bmax = std::max<uint64_t>(bmax, q.beams[t]);
+      hsum += q.beams[t];
+    }
+    if (first_bad != batch) break;
+    if (!q.topk_id_rows && (!q.topk_id || !q.topk_logp)) {
+      bad(FT_E_ARG, who() + "null topk arrays");
+      break;
+    }
+    if (q.topk_id_rows && !q.topk_logp_rows) {
+      bad(FT_E_ARG, who() + "null topk_logp rows");
+      break;
+    }
+    // the block: lnf[T + 1] f64, beams[T], rows (token, logp, index), key
+    // bounds; it must fit before anything is written
+    uint64_t o = align_up(8ull * (T + 1), 16);
+    d.beams_off = (uint32_t)o;
+    o = align_up(o + 4ull * T, 16);
+    d.rid_off = (uint32_t)o;
+    o = align_up(o + 4ull * T * K, 16);
+    d.rlp_off = (uint32_t)o;
+    o = align_up(o + 4ull * T * K, 16);
+    d.rk_off = (uint32_t)o;
+    o = align_up(o + 2ull * T * K, 16);
+    d.kb_off = (uint32_t)o;
+    o = align_up(o + 16ull * T, 16);
+    if (off + o > cap) {
+      bad(FT_E_LIMIT, who() + "the staged batch exceeds the staging buffer (" +
+                          std::to_string(cap) + " bytes)");
+      break;
+    }
     d.T = T;
     d.K = K;
     d.F = F;
@@ -758,111 +932,23 @@ static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& l
     d.sent_thr = q.sent_logp_threshold;
     d.in_off = off;
     d.out_T = T;
-    uint8_t* base = H + off;
-    uint64_t o = 0;
-    // length-norm table, exactly Agent::logp_norm's factor (agent.h:69-72)
-    double* lnf = (double*)(base + o);
-    // (depth 0 is the root alone, whose norm is never compared)
-    for (uint32_t dd = 0; dd <= T; ++dd) {
-      lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
-      if (dd > 0 && !std::isfinite(lnf[dd]))
-        return fail(FT_E_INPUT, who() + "length_norm gives a non-finite factor");
-    }
-    o = align_up(o + 8ull * (T + 1), 16);
-    d.beams_off = (uint32_t)o;
-    std::memcpy(base + o, q.beams, 4ull * T);
-    o = align_up(o + 4ull * T, 16);
-    d.rid_off = (uint32_t)o;
-    uint32_t* rid_s = (uint32_t*)(base + o);
-    o = align_up(o + 4ull * T * K, 16);
-    d.rlp_off = (uint32_t)o;
-    float* rlp_s = (float*)(base + o);
-    o = align_up(o + 4ull * T * K, 16);
-    d.rk_off = (uint32_t)o;
-    uint16_t* rk_s = (uint16_t*)(base + o);
-    o = align_up(o + 2ull * T * K, 16);
-    // rows in ascending token order, with each proposal's index in the
-    // caller's row (the order the reference visits proposals in)
-    for (uint32_t t = 0; t < T; ++t) {
-      const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
-      const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
-      if (!rid || !rlp) return fail(FT_E_ARG, who() + "null topk row");
-      bool sorted = true;
-      for (uint32_t k = 0; k < K; ++k) {
-        const float x = rlp[k];
-        if (std::isnan(x) || x == std::numeric_limits<float>::infinity())
-          return fail(FT_E_INPUT, who() + "topk_logp holds NaN or +inf");
-        if (k && rid[k] <= rid[k - 1]) sorted = false;
-      }
-      uint32_t* oid = rid_s + (uint64_t)t * K;
-      float* olp = rlp_s + (uint64_t)t * K;
-      uint16_t* ok = rk_s + (uint64_t)t * K;
-      if (sorted) {
-        std::memcpy(oid, rid, 4ull * K);
-        std::memcpy(olp, rlp, 4ull * K);
-        for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
-        continue;
-      }
-      for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
-      std::sort(tmp, tmp + K);
-      for (uint32_t p = 0; p < K; ++p) {
-        if (p && tmp[p].first == tmp[p - 1].first)
-          return fail(FT_E_INPUT, who() + "duplicate token id " +
-                                      std::to_string(tmp[p].first) +
-                                      " in topk row " + std::to_string(t));
-        oid[p] = tmp[p].first;
-        olp[p] = rlp[tmp[p].second];
-        ok[p] = (uint16_t)tmp[p].second;
-      }
-    }
-    // Per step, bounds of the keys pushed into `next`: a push's score is a
-    // parent score plus a logp that passes the token threshold, and itself
-    // passes the sentence threshold; parent scores are bounded by the same
-    // recursion one step earlier.  Double additions and the multiplication
-    // by the length factor are monotone, so the bounds hold exactly for the
-    // device's arithmetic (which this repeats).
-    d.kb_off = (uint32_t)o;
-    uint64_t* kb = (uint64_t*)(base + o);
-    o = align_up(o + 16ull * T, 16);
-    {
-      double s_lo = 0.0, s_hi = 0.0;  // parent scores at step t
-      for (uint32_t t = 0; t < T; ++t) {
-        const float* rlp = rlp_s + (uint64_t)t * K;
-        double x_lo = 0.0, x_hi = 0.0;
-        bool any = false;
-        for (uint32_t k = 0; k < K; ++k) {
-          const double x = (double)rlp[k];
-          if (x <= (double)q.token_logp_threshold) continue;  // never pushed
-          if (!any || x < x_lo) x_lo = x;
-          if (!any || x > x_hi) x_hi = x;
-          any = true;
-        }
-        const double lo = std::max(q.sent_logp_threshold, s_lo + x_lo);
-        const double hi = s_hi + x_hi;
-        kb[2 * t] = host_norm_key(lo * lnf[t + 1]);
-        kb[2 * t + 1] = host_norm_key(hi * lnf[t + 1]);
-        s_lo = lo;
-        s_hi = hi;
-      }
-    }
+    D[r] = d;
     off = align_up(off + o, 256);
-    if (off > cap) return fail(FT_E_LIMIT, "ft_stage: staging overflow");
     st.T = T;
     st.K = K;
     st.F = F;
-    {
-      uint64_t bmax = F, hsum = 0;
-      for (uint32_t t = 0; t < T; ++t) {
-        bmax = std::max<uint64_t>(bmax, q.beams[t]);
-        hsum += q.beams[t];
-      }
-      st.bmax = bmax;
-      st.hsum = hsum;
-    }
+    st.bmax = bmax;
+    st.hsum = hsum;
     st.out_bytes = step_stats_offset(F, T) + 8ull * kStepStats * T;
     max_out = std::max(max_out, st.out_bytes);
-    D[r] = d;
   }
+  // the blocks of the requests before the first shape error
+  for (size_t r = 0; r < first_bad; ++r) {
+    if (staged[r].skip) continue;
+    std::string msg;
+    if (int rc = pack_request(reqs[r], r, D[r], H + D[r].in_off, tmp, &msg)) return fail(rc, msg);
+  }
+  if (first_bad != batch) return fail(first_rc, first_msg);
   *out_stride = align_up(max_out, 256);
   *bytes = off;
   return FT_OK;

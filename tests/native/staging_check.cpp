@@ -1,0 +1,137 @@
+// Differential check of the request packing in ft_runtime.cpp (host code,
+// no GPU): random requests -- sorted and unsorted rows, ragged lengths,
+// thresholds that keep all, some or none of a row -- are packed by
+// pack_batch and compared with a plain scalar restatement of the staging
+// format (rows in ascending token order with each proposal's index in the
+// caller's row, the length-norm table, beam widths, and the per-step key
+// bounds).  Requests with NaN / +inf logps or duplicate token ids must fail.
+#include "ft_runtime.cpp"
+
+#include <cstdio>
+#include <random>
+
+namespace ftk {  // the device side is not linked here
+hipError_t launch_tbs(const KArgs&, hipStream_t) { return hipErrorUnknown; }
+hipError_t clear_controls(uint8_t*, uint64_t, uint64_t, uint32_t, hipStream_t) {
+  return hipErrorUnknown;
+}
+hipError_t scratch_address(int, void**) { return hipErrorUnknown; }
+int tbs_max_resident_blocks(int) { return 0; }
+}  // namespace ftk
+
+static int fails = 0;
+#define CHECK(c, ...)                      \
+  do {                                     \
+    if (!(c)) {                            \
+      if (fails++ < 10) {                  \
+        std::printf("FAIL %s: ", #c);      \
+        std::printf(__VA_ARGS__);          \
+        std::printf("\n");                 \
+      }                                    \
+    }                                      \
+  } while (0)
+
+int main() {
+  std::mt19937_64 g(12345);
+  std::vector<uint8_t> H(8 << 20);
+  std::vector<StagedReq> st(8);
+  std::vector<std::pair<uint32_t, uint32_t>> tmp(4096);
+  int cases = 0, rejected = 0;
+  for (int c = 0; c < 3000; ++c) {
+    const uint32_t T = 1 + g() % 6, K = 1 + g() % 70, n = 1 + g() % 4;
+    const float thr = -(float)(g() % 12);
+    const double sent = -(double)(g() % 30), alpha = (double)(g() % 6);
+    std::vector<std::vector<uint32_t>> beams(n), ids(n);
+    std::vector<std::vector<float>> lps(n);
+    std::vector<ft_request> reqs(n);
+    int expect_bad = 0;  // 1: NaN/inf, 2: duplicate
+    for (uint32_t r = 0; r < n; ++r) {
+      beams[r].resize(T);
+      for (auto& b : beams[r]) b = 1 + g() % 9;
+      ids[r].resize((size_t)T * K);
+      lps[r].resize((size_t)T * K);
+      for (uint32_t t = 0; t < T; ++t) {
+        uint32_t v = (uint32_t)(g() % 5) | ((g() % 8 == 0) ? 0x80000000u : 0u);
+        for (uint32_t k = 0; k < K; ++k) {
+          v += 1 + (uint32_t)(g() % 4);
+          ids[r][t * K + k] = v;
+          lps[r][t * K + k] = -(float)(g() % 60) * 0.25f;
+        }
+        if (g() % 3 == 0)  // shuffle: an unsorted row
+          std::shuffle(ids[r].begin() + t * K, ids[r].begin() + (t + 1) * K, g);
+        if (K > 1 && g() % 40 == 0) {
+          ids[r][t * K + 1] = ids[r][t * K];
+          expect_bad = expect_bad ? expect_bad : 2;
+        }
+        if (g() % 60 == 0) {
+          lps[r][t * K + g() % K] = (g() % 2) ? NAN : INFINITY;
+          expect_bad = expect_bad ? expect_bad : 1;
+        }
+      }
+      ft_request& q = reqs[r];
+      std::memset(&q, 0, sizeof q);
+      q.beams = beams[r].data();
+      q.num_beams = T;
+      q.num_steps = T;
+      q.topk = K;
+      q.topk_id = ids[r].data();
+      q.topk_logp = lps[r].data();
+      q.token_logp_threshold = thr;
+      q.sent_logp_threshold = sent;
+      q.length_norm = alpha;
+    }
+    for (auto& s : st) s = StagedReq();
+    uint64_t used = 0, ostride = 0;
+    StageLimits lim{64, 4096, 1000, 1u << 20};
+    const int rc = pack_batch(reqs.data(), n, lim, H.data(), H.size(), st.data(), tmp.data(),
+                              &used, &ostride);
+    if (expect_bad) {
+      CHECK(rc == FT_E_INPUT, "case %d: rc %d, expected an input error", c, rc);
+      ++rejected;
+      continue;
+    }
+    CHECK(rc == FT_OK, "case %d: rc %d %s", c, rc, g_err.c_str());
+    if (rc) continue;
+    ++cases;
+    const DevReq* D = (const DevReq*)H.data();
+    for (uint32_t r = 0; r < n; ++r) {
+      const DevReq& d = D[r];
+      const uint8_t* base = H.data() + d.in_off;
+      CHECK(d.T == T && d.K == K && d.F == beams[r][T - 1], "case %d header", c);
+      const double* lnf = (const double*)base;
+      for (uint32_t dd = 0; dd <= T; ++dd)
+        CHECK(lnf[dd] == std::pow(6.0 / (5.0 + dd), alpha), "case %d lnf", c);
+      CHECK(std::memcmp(base + d.beams_off, beams[r].data(), 4 * T) == 0, "case %d beams", c);
+      const uint32_t* rid = (const uint32_t*)(base + d.rid_off);
+      const float* rlp = (const float*)(base + d.rlp_off);
+      const uint16_t* rk = (const uint16_t*)(base + d.rk_off);
+      const uint64_t* kb = (const uint64_t*)(base + d.kb_off);
+      double s_lo = 0.0, s_hi = 0.0;
+      for (uint32_t t = 0; t < T; ++t) {
+        std::vector<std::pair<uint32_t, uint32_t>> e(K);
+        for (uint32_t k = 0; k < K; ++k) e[k] = {ids[r][t * K + k], k};
+        std::sort(e.begin(), e.end());
+        double x_lo = 0.0, x_hi = 0.0;
+        bool any = false;
+        for (uint32_t p = 0; p < K; ++p) {
+          CHECK(rid[t * K + p] == e[p].first && rk[t * K + p] == e[p].second &&
+                    rlp[t * K + p] == lps[r][t * K + e[p].second],
+                "case %d row %u pos %u", c, t, p);
+          const double x = (double)lps[r][t * K + p];
+          if (x <= (double)thr) continue;
+          if (!any || x < x_lo) x_lo = x;
+          if (!any || x > x_hi) x_hi = x;
+          any = true;
+        }
+        const double lo = std::max(sent, s_lo + x_lo), hi = s_hi + x_hi;
+        CHECK(kb[2 * t] == host_norm_key(lo * lnf[t + 1]) &&
+                  kb[2 * t + 1] == host_norm_key(hi * lnf[t + 1]),
+              "case %d bounds of step %u", c, t);
+        s_lo = lo;
+        s_hi = hi;
+      }
+    }
+  }
+  std::printf("%d batches packed, %d rejected, %d failures\n", cases, rejected, fails);
+  return fails ? 1 : 0;
+}
