@@ -80,6 +80,9 @@ struct alignas(16) Smem {
   unsigned long long bcast;
   uint32_t hstep[6];  // a helper's view of the posted step
   uint32_t multi_item;  // some parent of the step has other than one item
+  // the single-wave tail (tiny steps): where it stopped, for every thread
+  uint32_t tiny_t, tiny_ncur, tiny_nS, tiny_hist, tiny_done;
+  unsigned long long tiny_cands, tiny_ticks;
   uint32_t par_w;       // work items of a step with at most 64 parents
   uint32_t w_children, w_probes;
   // expansion: the current proposal row in ascending token order
@@ -1233,6 +1236,222 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
   }
 }
 
+// The single-wave tail of a request's search (see the leader's step loop):
+// wave 0 of the leader, lane j holding hypothesis j (j < n_cur) of a beam
+// of link parents whose parent table for step t0 is in LDS, and row t0 in
+// LDS.  Runs steps t0, t0 + 1, ... while every push survives: the
+// hypothesis's pending key token is looked up in the row, thresholds
+// applied (louds-trie.cc:87-90), and the extension goes to `selected` when
+// it completes the key (louds-trie.cc:97-102), else stays a link parent in
+// `next`.  Survivors keep their lanes (ranks among the live lanes give
+// their beam and history positions); the next row is read into registers
+// during a step and written to LDS at its end.  Stops (sm.tiny_done) when
+// the beam empties, the steps run out, or early exit fills `selected`; or
+// hands back (sm.tiny_done = 0) at the first step whose pushes overflow a
+// heap (bounded selection), would cut `selected` under early exit, or hit
+// a capacity limit -- then the beam is written to cur and the LDS / global
+// parent table of that step, which the general step reruns from scratch.
+// A value every lane of the wave holds alike, marked so: what is derived
+// from it can live in scalar registers rather than vector ones.
+__device__ __forceinline__ uint32_t uni(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+__device__ __forceinline__ uint64_t uni(uint64_t x) {
+  return (uint64_t)uni((uint32_t)x) | ((uint64_t)uni((uint32_t)(x >> 32)) << 32);
+}
+__device__ __forceinline__ float uni(float x) { return __uint_as_float(uni(__float_as_uint(x))); }
+__device__ __forceinline__ double uni(double x) {
+  return __longlong_as_double((long long)uni((uint64_t)__double_as_longlong(x)));
+}
+// second row buffer of the tiny steps, inside the LDS row arrays (rows of
+// at most kBlock proposals)
+constexpr uint32_t kTinyRowBuf = kBlock;
+static_assert(2 * kTinyRowBuf <= kMaxLdsTopk, "two tiny-step row buffers fit the LDS row");
+
+__device__ __forceinline__ void tiny_steps(
+    const KArgs& a, const DevReq& d, uint32_t t, uint32_t n_cur, uint32_t nS,
+    uint32_t hist_used, uint32_t lane, const double* lnf, const uint32_t* beams,
+    const uint32_t* rid, const float* rlp, CurRec* cur, SelRec* selA, HistRec* hist,
+    uint32_t* par_c0, uint32_t* par_aux, uint32_t* par_node, uint32_t* par_mode,
+    uint64_t* step_stats, Smem& sm) {
+  const uint32_t T = d.T, K = d.K, F = d.F;
+  const bool early = (d.flags & kReqEarlyExit) != 0;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  // this lane's hypothesis
+  bool alive = lane < n_cur;
+  uint32_t node = 0, hst = kNoHist, mode = M_LP_NEXT, sd = 0, ptok = 0, tc = kNoCursor;
+  double s = 0.0;
+  if (alive) {
+    node = sm.p_node[lane];
+    s = sm.p_s[lane];
+    hst = sm.p_hist[lane];
+    mode = sm.p_mode[lane] & kModeMask;
+    sd = sm.p_c0[lane];
+    ptok = sm.p_aux[lane];
+    tc = sm.p_lp[lane];
+  }
+  uint32_t status = 0;
+  bool done = false;
+  unsigned long long cands = 0, ticks = 0;
+  constexpr int kPf = kBlock / 64;  // row entries per lane
+  uint32_t cb = 0;  // row buffer of the current step: row_id / row_lp + cb
+  for (; t < T; ++t) {
+    if (n_cur == 0 || (early && nS >= F)) {
+      done = true;
+      break;
+    }
+    const unsigned long long c0 = wall_clock64();
+    const bool more = t + 1 < T;
+    // the next row straight into the other LDS row buffer (no registers),
+    // while this step searches its own
+    const uint32_t nb = kTinyRowBuf - cb;
+    if (more) {
+      const uint64_t ro = (uint64_t)(t + 1) * K;
+#pragma unroll
+      for (int i = 0; i < kPf; ++i) {
+        const uint32_t k = min((uint32_t)i * 64u + lane, K - 1u);
+        __builtin_amdgcn_global_load_lds(rid + ro + k, &sm.row_id[nb + (uint32_t)i * 64u], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(rlp + ro + k, &sm.row_lp[nb + (uint32_t)i * 64u], 4, 0, 0);
+      }
+    }
+    // the pending token in the row, thresholds in double (`<=` drops)
+    bool pass = false;
+    double s2 = 0.0;
+    int pos = -1;
+    if (alive) {
+      uint32_t lo = 0, hi = K;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (sm.row_id[cb + mid] < ptok) lo = mid + 1; else hi = mid;
+      }
+      pos = (lo < K && sm.row_id[cb + lo] == ptok) ? (int)lo : -1;
+      if (pos >= 0) {
+        const float x = sm.row_lp[cb + (uint32_t)pos];
+        pass = !(((double)x <= (double)d.tok_thr) || (s + (double)x <= d.sent_thr));
+        s2 = s + (double)x;
+      }
+    }
+    const bool to_sel = pass && mode == M_LP_SEL;
+    const bool to_next = pass && mode == M_LP_NEXT;
+    const uint64_t mS = __ballot(to_sel), mN = __ballot(to_next);
+    const uint32_t n_new = (uint32_t)__popcll(mS), n_next = (uint32_t)__popcll(mN);
+    const uint32_t Mnext = beams[t];
+    // every push survives and no limit is reached, or hand back (after the
+    // row reads into LDS have landed)
+    if (n_next > Mnext || nS + n_new > F || nS + n_new > a.lay.sel_cap ||
+        hist_used + n_next > a.lay.hist_cap) {
+      wait_stores();
+      break;
+    }
+    // early exit with `selected` exactly full: every new push is among the
+    // first F (louds-trie.cc:81-83), and the search ends after this step
+    const bool stop_early = early && nS + n_new >= F;
+    if (to_sel) {
+      SelRec sr;
+      sr.s = s2;
+      sr.node = node;
+      sr.depth = t + 1;
+      sr.phist = hst;
+      sr.tok = ptok;
+      sr.jk = 0;
+      sr.isnew = 0;  // kept: `selected` has room for every push
+      st_sel(&selA[nS + (uint32_t)__popcll(mS & lt)], sr);
+    }
+    if (stop_early) {  // selected is full: the search ends here
+      nS += n_new;
+      cands += n_new;
+      if (lane == 0 && t < d.out_T) {
+        uint64_t* row = step_stats + (uint64_t)t * kStepStats;
+        row[0] = n_cur;
+        row[1] = n_cur;
+        row[2] = n_next;
+        row[3] = n_new;
+        row[4] = wall_clock64() - c0;
+      }
+      ticks += wall_clock64() - c0;
+      wait_stores();
+      done = true;
+      break;
+    }
+    if (to_next) {
+      const uint32_t o = hist_used + (uint32_t)__popcll(mN & lt);
+      HistRec h;
+      h.phist = hst;
+      h.tok = ptok;
+      hist[o] = h;
+      hst = o;
+      s = s2;
+      // the pending token of step t + 1: on the node's own edge the next
+      // tail token, else the walk parent_entry makes
+      if (tc != kNoCursor) {
+        ++tc;
+        ptok = a.tail[tc];
+        mode = (t + 2 == sd) ? M_LP_SEL : M_LP_NEXT;
+      } else {
+        // (what parent_entry builds for a link parent at step t + 1)
+        uint32_t err = 0;
+        const ft_node_rec r = a.recs[node];
+        ptok = kb_token(a, node, r, t + 1, &err);
+        if (err) status |= kStatusCorrupt;
+        mode = (t + 2 == sd) ? M_LP_SEL : M_LP_NEXT;
+        const uint32_t el = (r.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+        tc = ((r.meta & FT_META_LINK) && t + 1 + el >= sd) ? r.tail_off + (t + 1 + el - sd)
+                                                           : kNoCursor;
+      }
+    }
+    alive = to_next;
+    if (lane == 0 && t < d.out_T) {
+      uint64_t* row = step_stats + (uint64_t)t * kStepStats;
+      row[0] = n_cur;
+      row[1] = n_cur;
+      row[2] = n_next;
+      row[3] = n_new;
+      row[4] = wall_clock64() - c0;
+    }
+    hist_used += n_next;
+    nS += n_new;
+    cands += (uint64_t)n_next + n_new;
+    if (lane == 0) sm.cnt_parents += n_cur;
+    n_cur = n_next;
+    // the next row has landed in the other buffer (and this step's stores
+    // are complete)
+    wait_stores();
+    cb = nb;
+    ticks += wall_clock64() - c0;
+    if (status) break;
+  }
+  if (t >= T) done = true;
+  const uint64_t am = __ballot(alive);
+  if (!done && !status) {
+    // hand the beam back: hypothesis of lane j at position rank(j)
+    if (alive) {
+      const uint32_t o = (uint32_t)__popcll(am & lt);
+      st_cur(&cur[o], s, node, hst);
+      sm.p_node[o] = node;
+      sm.p_s[o] = s;
+      sm.p_hist[o] = hst;
+      sm.p_mode[o] = (uint8_t)mode;
+      sm.p_c0[o] = sd;
+      sm.p_aux[o] = ptok;
+      sm.p_lp[o] = tc;
+      st_dev(&par_c0[o], sd);
+      st_dev(&par_aux[o], ptok);
+      st_dev(&par_node[o], node);
+      st_dev(&par_mode[o], mode);
+    }
+  }
+  if (lane == 0) {
+    sm.tiny_t = t;
+    sm.tiny_ncur = n_cur;
+    sm.tiny_nS = nS;
+    sm.tiny_hist = hist_used;
+    sm.tiny_done = done ? 1u : 0u;
+    sm.tiny_cands = cands;
+    sm.tiny_ticks = ticks;
+    if (status) sm.status |= status;
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   __shared__ Smem sm;
   // request-major interleave: request r owns blocks r, r + batch, ...  The
@@ -1261,7 +1480,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   // ---- the leader ----------------------------------------------------------
   uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
   OutHeader* oh = (OutHeader*)ob;
-  const uint8_t* in = a.stage + d.in_off;
+  const uint8_t* in = a.stage + uni(d.in_off);
   const double* lnf = (const double*)in;
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
@@ -1332,6 +1551,46 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
 
   for (uint32_t t = 0; t < T; ++t) {
     if (n_cur == 0 || (early && nS >= F)) break;
+    // ---- the tail of small link-parent steps, on one wave ---------------
+    // When the beam holds at most 64 hypotheses and every one is a link
+    // parent (it can only continue with its own next key token,
+    // louds-trie.cc:91-102), each step is one row lookup per hypothesis.
+    // A link parent either stays one (next) or closes its key (selected),
+    // so the beam stays in this form until it empties.  Wave 0 runs these
+    // steps alone, the hypotheses in its lanes' registers, without block
+    // barriers, for as long as every push survives both heaps (no bounded
+    // selection cuts and early exit does not fire mid-step); at the first
+    // step that needs a cut it hands the beam back to the general step.
+    if (par_ready && n_cur <= 64u && K <= (uint32_t)kBlock) {
+      const uint32_t lane = tid & 63u;
+      const uint32_t md0 = lane < n_cur ? (uint32_t)(sm.p_mode[lane] & kModeMask) : (uint32_t)M_LP_NEXT;
+      if (__ballot(md0 != M_LP_NEXT && md0 != M_LP_SEL) == 0) {
+        if (row_pf) {
+          if (tid < K) {
+            sm.row_id[tid] = pf_id;
+            sm.row_lp[tid] = pf_lp;
+          }
+        } else {
+          load_row(rid, rlp, t, K, sm);
+        }
+        __syncthreads();
+        if (tid < 64u) tiny_steps(a, d, t, n_cur, nS, hist_used, lane, lnf, beams, rid, rlp,
+                                  cur, selA, hist, par_c0, par_aux, par_node, par_mode,
+                                  step_stats, sm);
+        __syncthreads();
+        t = sm.tiny_t;
+        n_cur = sm.tiny_ncur;
+        nS = sm.tiny_nS;
+        hist_used = sm.tiny_hist;
+        n_cands += sm.tiny_cands;
+        t_exp += sm.tiny_ticks;
+        if (sm.tiny_done || sm.status) break;
+        // a cut is due at step t: the general step below runs it, with the
+        // beam handed back in the parent table and row t reloaded
+        row_pf = false;
+        if (n_cur == 0 || (early && nS >= F)) break;
+      }
+    }
     const unsigned long long t0 = wall_clock64();
     const uint32_t ncur0 = n_cur;
     if (row_pf) {
@@ -1348,6 +1607,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // work items of parent j (j < n_cur), writing its table entry unless the
     // previous step's emit did
     auto parent_work = [&](uint32_t j) -> uint32_t {
+      // (an opaque index: the per-thread addresses below are formed here,
+      // not hoisted out of the step loop into registers held all along)
+      asm volatile("" : "+v"(j));
       const bool lp = n_cur <= (uint32_t)kBlock;
       if (par_ready) {
         if (lp) {
@@ -1394,7 +1656,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         const uint32_t incl = wave_incl_scan(work);
         const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
         if (tid < n_cur) {
-          st_dev(&par_woff[tid], incl - work);
+          uint32_t j = tid;
+          asm volatile("" : "+v"(j));  // (address formed here, not held)
+          st_dev(&par_woff[j], incl - work);
           sm.woff[tid] = incl - work;
           if (work != 1) sm.multi_item = 1;  // cleared before the step began
         }
