@@ -3,7 +3,7 @@
 // Owns the trie image in HBM, the per-request workspace (allocated once by
 // ft_reserve, like LoudsTrie::init_tbs_gpu, tbs-kernels.cu:599-648), the
 // pinned staging buffers and the stream.  A batch is packed into one pinned
-// buffer, copied with one H2D, searched by one cooperative launch and copied
+// buffer, copied with one H2D, searched by one kernel launch and copied
 // back with one D2H (compare the per-request launches of tbs_gpu_batched,
 // tbs-kernels.cu:686-700).
 #include <hip/hip_runtime.h>
@@ -106,6 +106,9 @@ struct ft_ctx {
   uint32_t wgs_req = 4096;    // workgroups per request (clamped to residency:
                               // a lone request gets every CU)
   uint32_t share_min = 4096;  // work items from which a step is shared
+  // test knob: helpers never claim their slices, so the leader takes every
+  // one over after its grace period
+  uint32_t no_claims = 0;
   int max_resident = 0;
   // this device's no-allocation scratch (looked up at ft_create), or null
   // with the reason in scratch_err
@@ -523,9 +526,6 @@ int ft_create(const void* image, size_t image_bytes, int device,
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(FT_E_DEVICE, std::string("ft_create: device is ") +
                                  prop.gcnArchName + ", this build targets gfx950");
-  int coop = 0;
-  (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
-  if (!coop) return fail(FT_E_DEVICE, "ft_create: no cooperative launch");
 
   auto* c = new ft_ctx();
   c->device = device;
@@ -582,6 +582,7 @@ int ft_create(const void* image, size_t image_bytes, int device,
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0) c->share_min = (uint32_t)v;
   }
+  if (const char* s = std::getenv("FT_TEST_NO_CLAIMS")) c->no_claims = std::atoi(s) ? 1u : 0u;
   if (const char* s = std::getenv("FT_SCAN_MULT")) {
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
@@ -600,7 +601,8 @@ static std::atomic<uint32_t> g_launch_epoch{0};
 // hypotheses, rows of at most K proposals and `hist` history records; the
 // candidate lists are sized so that no push can overflow (B * K pushes into
 // `next`, B * K + B into `selected`).  Returns the slot stride.
-static uint64_t ws_layout(uint64_t B, uint64_t K, uint64_t hist, WsLayout* out) {
+static uint64_t ws_layout(uint64_t B, uint64_t K, uint64_t hist, uint32_t slots,
+                          WsLayout* out) {
   const uint64_t BK = B * K;
   WsLayout L{};
   uint64_t off = 0;
@@ -617,6 +619,8 @@ static uint64_t ws_layout(uint64_t B, uint64_t K, uint64_t hist, WsLayout* out) 
   L.par_node = off; off = align_up(off + B * 4, 256);
   L.par_mode = off; off = align_up(off + B * 4, 256);
   L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
+  L.claims = off; off = align_up(off + (uint64_t)slots * 8, 256);
+  L.claim_slots = slots;
   L.next_cap = (uint32_t)BK;
   L.sel_cap = (uint32_t)(BK + B);
   L.hist_cap = (uint32_t)hist;
@@ -649,7 +653,7 @@ int ft_reserve(ft_ctx* c, size_t max_batch, size_t max_topk, size_t max_steps,
   release_workspace(c);
   const uint64_t B = max_out_beams, K = max_topk;
   if (B * K + B >= 0xFFFFFFF0ull) return fail(FT_E_LIMIT, "ft_reserve: beams * topk too large");
-  c->ws_stride = ws_layout(B, K, max_inter_beams, &c->lay);
+  c->ws_stride = ws_layout(B, K, max_inter_beams, (uint32_t)c->max_resident, &c->lay);
   c->out_slot_max = align_up(step_stats_offset((uint32_t)B, 0) + 4 * (uint64_t)max_out_tokens +
                                  8ull * kStepStats * max_steps + 8, 256);
   // per request: lnf + beams + sorted rows (token, logp, index) + key bounds
@@ -1010,7 +1014,7 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.scan_limit = (uint32_t)std::min<uint64_t>(sl, 0xFFFFFFFFull);
   // helpers per request: as many as stay co-resident with the batch
   const uint32_t fit = (uint32_t)std::max<int>(1, c->max_resident / (int)count);
-  a.wgs = std::max(1u, std::min(c->wgs_req, fit));
+  a.wgs = std::max(1u, std::min(std::min(c->wgs_req, fit), lay.claim_slots));
   a.share_min = c->share_min;
   uint32_t ep = ++g_launch_epoch;
   if (ep == 0) ep = ++g_launch_epoch;
@@ -1021,17 +1025,18 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.labels = c->d_labels;
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
+  a.no_claims = c->no_claims;
   return a;
 }
 
-// One cooperative launch on the context stream, bracketed by a pair of the
+// One launch of the search kernel on the context stream, bracketed by a pair of the
 // ring's timing events.
 static int launch_timed(ft_ctx* c, const KArgs& a) {
   (void)hipSetDevice(c->device);
   const size_t slot = (c->launches % ft_ctx::kRing) * 2;
   (void)hipEventRecord(c->ring[slot], c->stream);
   hipError_t e = launch_tbs(a, c->stream);
-  if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel");
+  if (e != hipSuccess) return hip_fail(e, "launch of the search kernel");
   (void)hipEventRecord(c->ring[slot + 1], c->stream);
   ++c->launches;
   return FT_OK;
@@ -1261,7 +1266,7 @@ int ft_search_noalloc(ft_ctx* c, const ft_request* reqs, size_t batch,
   if (B * K + B >= 0xFFFFFFF0ull || H >= 0xFFFFFFF0ull)
     return fail(FT_E_LIMIT, "ft_search_noalloc: beams * topk too large");
   WsLayout L{};
-  const uint64_t ws_stride = ws_layout(B, K, H, &L);
+  const uint64_t ws_stride = ws_layout(B, K, H, (uint32_t)c->max_resident, &L);
   const uint64_t out_off = align_up(used, 256);
   const uint64_t ws_off = align_up(out_off + out_stride * batch, 256);
   const uint64_t total = ws_off + ws_stride * batch;
@@ -1272,9 +1277,10 @@ int ft_search_noalloc(ft_ctx* c, const ft_request* reqs, size_t batch,
   uint8_t* base = c->d_scratch;
   hipError_t e = hipMemcpyAsync(base, g_na_stage, used, hipMemcpyHostToDevice, c->stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(scratch stage)");
-  // the control blocks start at "nothing posted" (a fill kernel, no memset)
-  if ((e = clear_controls(base + ws_off, ws_stride, L.ctl, (uint32_t)batch, c->stream)) !=
-      hipSuccess)
+  // the control blocks and claim words start at "nothing posted" (a fill
+  // kernel, no memset)
+  if ((e = clear_controls(base + ws_off, ws_stride, L.ctl, L.claims, L.claim_slots,
+                          (uint32_t)batch, c->stream)) != hipSuccess)
     return hip_fail(e, "clear_controls");
   const KArgs a = kernel_args(c, base, 0, batch, (uint32_t)K, base + ws_off, ws_stride, L,
                               base + out_off, out_stride);

@@ -175,7 +175,11 @@ static_assert(sizeof(Ctl) == 384, "Ctl layout");
 struct WsLayout {   // byte offsets inside one request's workspace slot
   uint64_t cur0, cur1, nextc, selA, selB, rank, hist;
   uint64_t ctl, par_c0, par_aux, par_node, par_mode, par_woff;
+  // claim words of a shared step's slices, one per workgroup of the
+  // request: (launch epoch << 32) | generation of the step it was taken for
+  uint64_t claims;
   uint32_t next_cap, sel_cap, hist_cap, cur_cap;
+  uint32_t claim_slots, pad;
 };
 
 struct KArgs {
@@ -200,11 +204,14 @@ struct KArgs {
   uint32_t wgs;        // workgroups per request (1 leader + wgs-1 helpers)
   uint32_t share_min;  // work items from which a step is shared
   uint32_t epoch;      // launch counter (tags the control words)
-  uint32_t pad;
+  // helpers never claim their slices (a test of the leader's take-over of
+  // unclaimed slices; never set otherwise)
+  uint32_t no_claims;
 };
 
-// Launches the search over `batch` requests (wgs workgroups each) as a
-// cooperative launch on `stream`.
+// Launches the search over `batch` requests (wgs workgroups each) on
+// `stream` (an ordinary launch: no workgroup waits for one that may not be
+// resident, see tbs_kernel.hip).
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
 
 // The no-allocation scratch: one file-scope device array of this many
@@ -217,10 +224,11 @@ constexpr uint64_t kScratchBytes = 128ull << 20;
 // kept; later calls return the kept address.
 hipError_t scratch_address(int device, void** ptr);
 
-// Zeroes the control block (Ctl, at byte ctl_off) of `count` workspace
-// slots of `stride` bytes from `ws`, with a fill kernel on `stream`.
-hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint32_t count,
-                          hipStream_t stream);
+// Zeroes the control block (Ctl, at byte ctl_off) and the claim words
+// (claim_slots of them at claims_off) of `count` workspace slots of
+// `stride` bytes from `ws`, with a fill kernel on `stream`.
+hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64_t claims_off,
+                          uint32_t claim_slots, uint32_t count, hipStream_t stream);
 
 // Workgroups of the search kernel that fit on the device at once.
 int tbs_max_resident_blocks(int num_cus);

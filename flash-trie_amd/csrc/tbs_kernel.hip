@@ -1,10 +1,12 @@
 // tbs_kernel.hip -- trie beam search (TBS) kernel for gfx950 (MI355X).
 //
-// The whole batch is one cooperative launch with no host round trip between
+// The whole batch is one kernel launch with no host round trip between
 // decoding steps.  Each request has a leader workgroup of 1024 threads (16
 // wave64) that runs every step -- parent table, expansion, validation,
 // pruning -- and helper workgroups that join the expansion of the steps
-// with many work items.  Semantics are those of the reference CPU path
+// with many work items: each claims its slice of such a step, and the
+// leader takes over slices no helper has claimed, so the launch needs no
+// co-residency guarantee.  Semantics are those of the reference CPU path
 // LoudsTrie::tbs (lib/marisa/grimoire/trie/louds-trie.cc:75-177):
 //
 //  * cur is processed parent by parent in ascending (norm, node id) order and
@@ -78,7 +80,11 @@ struct alignas(16) Smem {
   uint32_t status;
   unsigned long long cnt_parents, cnt_children, cnt_probes;
   unsigned long long bcast;
-  uint32_t hstep[6];  // a helper's view of the posted step
+  uint32_t hstep[7];  // a helper's view of the posted step (+ whether it
+                      // took its slice)
+  uint32_t lead_flag;   // the leader's broadcast of a decision of thread 0
+  uint32_t n_stolen;    // helper slices the leader took over this step
+  uint16_t stolen[256];
   uint32_t multi_item;  // some parent of the step has other than one item
   // the single-wave tail (tiny steps): where it stopped, for every thread
   uint32_t tiny_t, tiny_ncur, tiny_nS, tiny_hist, tiny_done;
@@ -435,7 +441,7 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
     const uint64_t hi_mask = (top >= 63) ? 0ull : ~((2ull << top) - 1ull);
     for (uint32_t i = tid; i < nb; i += kBlock) sm.whist[i] = 0;
     __syncthreads();
-    visit_keys<8>(n, gk, [&](uint32_t, bool ok, uint64_t k) {
+    visit_keys<6>(n, gk, [&](uint32_t, bool ok, uint64_t k) {
       const uint64_t o = k - base;
       const bool act = ok && (o & hi_mask) == prefix;
       hist_add(act, (uint32_t)((o >> sh) & (nb - 1)), sm.whist);
@@ -825,6 +831,10 @@ __device__ __forceinline__ void wait_stores() {
 // Upper bound on spin iterations of a wait (each sleeps ~64 cycles): far
 // beyond any step, so a wait only ends this way if the peer is gone.
 constexpr uint32_t kSpinLimit = 1u << 28;
+// How long the leader waits for helpers to claim their slices of a shared
+// step before it takes the unclaimed ones over (wall-clock ticks of
+// 10 ns): running helpers claim within a few microseconds of the post.
+constexpr unsigned long long kGraceTicks = 5000;
 
 // Everything a workgroup needs to expand a range of work items of one step.
 struct StepView {
@@ -1143,24 +1153,42 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
         __builtin_amdgcn_s_sleep(1);
       }
       sm.bcast = v;
+      sm.hstep[6] = 0;
       if ((v >> 32) == a.epoch && (uint32_t)v != kGoExit && v != seen) {
         // the step's parameters, read once after `go` and shared through LDS
         // so that every thread takes the same branches below
-        sm.hstep[0] = ld_relaxed(&ctl->t);
-        sm.hstep[1] = ld_relaxed(&ctl->W);
-        sm.hstep[2] = ld_relaxed(&ctl->n_par);
-        sm.hstep[3] = ld_relaxed(&ctl->nS);
+        const uint32_t pt = ld_relaxed(&ctl->t), pW = ld_relaxed(&ctl->W),
+                       pn = ld_relaxed(&ctl->n_par), pS = ld_relaxed(&ctl->nS);
+        sm.hstep[0] = pt;
+        sm.hstep[1] = pW;
+        sm.hstep[2] = pn;
+        sm.hstep[3] = pS;
         sm.hstep[4] = ld_relaxed(&ctl->cur_which);
         sm.hstep[5] = ld_relaxed(&ctl->sel_which);
+        // Take this workgroup's slice of the step: its claim word goes from
+        // an older (epoch, generation) to this one, unless the leader took
+        // the slice over first (the word already holds this step or a
+        // later one).  A successful claim also proves the parameters just
+        // read are this step's: the leader writes the next step's only
+        // after every claimed slice is done.  A posted step always
+        // satisfies the bounds below; anything else is not taken.
+        const uint64_t max_w = (uint64_t)pn * max(a.scan_limit, d.K);
+        const bool sane = pt < d.T && pn != 0 && pn <= a.lay.cur_cap &&
+                          pS <= a.lay.sel_cap && (uint64_t)pW <= max_w;
+        unsigned long long* cl = (unsigned long long*)(ws + a.lay.claims) + g;
+        const unsigned long long c = ld_relaxed(cl);
+        if (sane && !a.no_claims && c < v && atomicCAS(cl, c, v) == c) sm.hstep[6] = 1;
       }
     }
     __syncthreads();
     const unsigned long long v = sm.bcast;
     const uint32_t t = sm.hstep[0], W = sm.hstep[1], n_par = sm.hstep[2],
                    nS = sm.hstep[3], cur_which = sm.hstep[4], sel_which = sm.hstep[5];
+    const bool mine = sm.hstep[6] != 0;
     __syncthreads();
     if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
     seen = v;
+    if (!mine) continue;  // the leader took this slice over
     StepView sv;
     sv.cur = (const CurRec*)(ws + (cur_which ? a.lay.cur1 : a.lay.cur0));
     sv.sel = (SelRec*)(ws + (sel_which ? a.lay.selB : a.lay.selA));
@@ -1177,12 +1205,6 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.nS = nS;
     sv.next_cap = a.lay.next_cap;
     sv.sel_cap = a.lay.sel_cap;
-    // a posted step always satisfies these bounds; anything else is not a
-    // step of this launch and is not expanded
-    const uint64_t max_w = (uint64_t)sv.n_par * max(a.scan_limit, d.K);
-    if (t >= d.T || sv.n_par == 0 || sv.n_par > a.lay.cur_cap ||
-        sv.nS > a.lay.sel_cap || (uint64_t)W > max_w)
-      continue;
     sv.lnf_next = lnf[t + 1];
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
@@ -1507,6 +1529,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
                  hist_cap = a.lay.hist_cap;
   const unsigned long long tag = (unsigned long long)a.epoch << 32;
   uint32_t gen = 0;
+  unsigned long long t_post = 0;  // (thread 0) wall clock of the last post
 
   unsigned long long t_exp = 0, t_sel = 0, t_all0 = wall_clock64();
   // per-step profile rows after the output tokens: kStepStats u64 per step
@@ -1739,7 +1762,11 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       }
       wait_stores();  // the step's data is complete before `go` moves
       __syncthreads();
-      if (tid == 0) st_dev(&ctl->go, tag | ++gen);
+      ++gen;
+      if (tid == 0) {
+        st_dev(&ctl->go, tag | gen);
+        t_post = wall_clock64();
+      }
     }
     // (the parent table ended synchronised: the row and the emptied hash are
     // visible)
@@ -1748,12 +1775,56 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared,
                  hashed, sm);
     if (shared) {
+      // The helpers' slices: each is claimed by its helper (its claim word
+      // set to this step) or, once kGraceTicks have passed since the post,
+      // taken over here -- so the step never waits for a workgroup that is
+      // not running.  Then every claimed slice is waited for: a helper that
+      // claimed one is running and finishes it.
+      const unsigned long long mygo = tag | gen;
+      unsigned long long* claims = (unsigned long long*)(ws + a.lay.claims);
+      const uint32_t nh = a.wgs - 1;  // helper slots 1 .. nh (nh < kBlock)
+      for (;;) {
+        const int pending = __syncthreads_count(tid < nh && ld_relaxed(&claims[tid + 1]) != mygo);
+        if (pending == 0) break;
+        if (tid == 0) sm.lead_flag = (wall_clock64() - t_post > kGraceTicks) ? 1u : 0u;
+        __syncthreads();
+        const bool expired = sm.lead_flag != 0;
+        __syncthreads();
+        if (expired) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (tid == 0) sm.n_stolen = 0;
+      __syncthreads();
+      if (tid < nh) {
+        unsigned long long* cl = &claims[tid + 1];
+        const unsigned long long c = ld_relaxed(cl);
+        if (c < mygo && atomicCAS(cl, c, mygo) == c) {
+          const uint32_t k = atomicAdd(&sm.n_stolen, 1u);
+          sm.stolen[k] = (uint16_t)(tid + 1);
+        }
+      }
+      __syncthreads();
+      const uint32_t n_stolen = sm.n_stolen;
+      for (uint32_t i = 0; i < n_stolen; ++i) {
+        const uint32_t slice = sm.stolen[i];
+        __syncthreads();
+        if (tid == 0) {
+          sm.w_children = 0;
+          sm.w_probes = 0;
+          sm.lq_next = 0;
+          sm.lq_sel = 0;
+        }
+        __syncthreads();
+        expand_range(a, sv, W, slice * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, true, false,
+                     hashed, sm);
+      }
       if (tid == 0) {
+        const uint32_t helped = nh - n_stolen;
         for (uint32_t it = 0; it < kSpinLimit; ++it) {
-          if (ld_relaxed(&ctl->done) >= a.wgs - 1) break;
+          if (ld_relaxed(&ctl->done) >= helped) break;
           __builtin_amdgcn_s_sleep(1);
         }
-        if (ld_relaxed(&ctl->done) < a.wgs - 1) sm.status |= kStatusCorrupt;
+        if (ld_relaxed(&ctl->done) < helped) sm.status |= kStatusCorrupt;
       }
     }
     __syncthreads();
@@ -2200,25 +2271,33 @@ hipError_t scratch_address(int device, void** ptr) {
   return hipSuccess;
 }
 
-// One workgroup per slot: the slot's control block, word by word.
+// One workgroup per slot: the slot's control block and claim words, word
+// by word.
 __global__ void __launch_bounds__(128) clear_ctl_kernel(uint8_t* ws, uint64_t stride,
-                                                        uint64_t ctl_off) {
-  uint32_t* p = (uint32_t*)(ws + (uint64_t)blockIdx.x * stride + ctl_off);
+                                                        uint64_t ctl_off, uint64_t claims_off,
+                                                        uint32_t claim_slots) {
+  uint8_t* slot = ws + (uint64_t)blockIdx.x * stride;
+  uint32_t* p = (uint32_t*)(slot + ctl_off);
   for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(Ctl) / 4); i += blockDim.x) p[i] = 0u;
+  unsigned long long* c = (unsigned long long*)(slot + claims_off);
+  for (uint32_t i = threadIdx.x; i < claim_slots; i += blockDim.x) c[i] = 0ull;
 }
 
-hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint32_t count,
-                          hipStream_t stream) {
+hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64_t claims_off,
+                          uint32_t claim_slots, uint32_t count, hipStream_t stream) {
   if (count == 0) return hipSuccess;
-  hipLaunchKernelGGL(clear_ctl_kernel, dim3(count), dim3(128), 0, stream, ws, stride, ctl_off);
+  hipLaunchKernelGGL(clear_ctl_kernel, dim3(count), dim3(128), 0, stream, ws, stride, ctl_off,
+                     claims_off, claim_slots);
   return hipGetLastError();
 }
 
+// An ordinary launch: the protocol of the shared steps never makes a
+// workgroup wait for one that is not running (helpers' slices are claimed,
+// and the leader takes over the slices no helper has claimed), so the grid
+// needs no co-residency guarantee.
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
-  void* params[] = {(void*)&args};
-  return hipLaunchCooperativeKernel((const void*)tbs_kernel,
-                                    dim3(args.batch * args.wgs), dim3(kBlock),
-                                    params, 0, stream);
+  hipLaunchKernelGGL(tbs_kernel, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream, args);
+  return hipGetLastError();
 }
 
 int tbs_block_threads() { return kBlock; }

@@ -89,9 +89,7 @@ def test_cli_usage_errors(ft, tmp_path):
 
 @pytest.mark.gpu
 def test_cli_gpu_matches_host(ft, tmp_path):
-    # The tool is a separate process: it can launch the search only while no
-    # other live process has made cooperative launches on the GPU (this file
-    # runs before the in-process GPU tests for that reason).
+    # The tool is a separate process searching on the GPU.
     write_dataset(ft, str(tmp_path))
     csv = tmp_path / "timing.csv"
     env = dict(os.environ, TBS_TIMING_CSV=str(csv))

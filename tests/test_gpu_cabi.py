@@ -1,7 +1,6 @@
 """The C ABI driven from ctypes, as another host language would: ft_create,
 ft_reserve, ft_search, and ft_stage / ft_launch_range / ft_fetch, against the
-oracle.  (This module sorts after the command line tool's test: once this
-process has made cooperative launches, another process cannot.)"""
+oracle; and a second process searching on the GPU while this one lives."""
 
 import ctypes
 
@@ -46,3 +45,24 @@ def test_c_abi_search_through_ctypes(ft, po):
         assert b.results(1)[0] == want[0]
     finally:
         lib.ft_destroy(ctx)
+
+
+@pytest.mark.gpu
+def test_second_process_searches_after_this_one(ft, tmp_path):
+    # launches are ordinary (no cooperative launch), so a second process can
+    # search on the GPU while this one, which has searched already, lives
+    import subprocess
+
+    from test_cli import CLI, write_dataset
+    t = ft.Trie()
+    t.build([[1, 2, 3, 4], [1, 2, 3, 5], [7]])
+    t.init_tbs_gpu(1, max_num_topk=8, max_num_outpos=4, max_num_out_beams=8,
+                   max_num_out_tokens=32, max_num_inter_beams=64)
+    got = ft.bs_tbs_gpu(t, 1, [[10] * 4], [[[1, 2, 3, 4, 5, 7]] * 4],
+                        [[[-0.5, -3, -3, -3, -3, -1.0]] * 4], -10.0, -40.0, 0.0, False)
+    assert got[0][0]
+    write_dataset(ft, str(tmp_path))
+    p = subprocess.run([CLI, "-g", "-a", str(tmp_path), "8", "4"], capture_output=True,
+                       text=True, timeout=300)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert "12/12 requests identical on CPU and GPU" in p.stdout

@@ -296,6 +296,33 @@ def test_shared_steps(ft, po, monkeypatch, wgs, share_min):
                                     f"wgs {wgs} req {b0 + i} {alpha} {early}")
 
 
+@pytest.mark.parametrize("wgs", ["2", "16"])
+def test_leader_takes_over_unclaimed_slices(ft, po, monkeypatch, wgs):
+    # helpers that never claim their slices of a shared step (a test knob):
+    # after its grace period the leader takes every slice over and expands
+    # it itself -- the step never waits for a workgroup that is not running
+    monkeypatch.setenv("FT_WGS", wgs)
+    monkeypatch.setenv("FT_SHARE_MIN", "0")
+    monkeypatch.setenv("FT_TEST_NO_CLAIMS", "1")
+    toks, offs = ft.synth_keys(40000, 4096, 3, 8, 1.1, 13)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=2, topk=64, steps=8,
+                  beams=32, inter=4096)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 6, 4096, 8, 64, 32, 0.3, 2.0, True, 13,
+                                model=1)
+    for b0 in range(0, 6, 2):
+        for early in (False, True):
+            got = ft.bs_tbs_gpu(t, 2, [[32] * 8] * 2,
+                                [ids[b0 + i].tolist() for i in range(2)],
+                                [lp[b0 + i].tolist() for i in range(2)],
+                                -10.0, -40.0, 5.0, early)
+            for i in range(2):
+                want = o.tbs([32] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0,
+                             5.0, early)
+                assert_same_results((got[0][i], got[1][i]), want,
+                                    f"no claims, wgs {wgs} req {b0 + i} {early}")
+
+
 def test_fresh_contexts_shared_steps(ft, po, monkeypatch):
     # contexts created and destroyed one after another, every step shared: a
     # new workspace may sit on memory an earlier context used, so its control

@@ -157,8 +157,8 @@ def test_sweep_cpu(ft, example, tmp_path):
 
 @pytest.mark.gpu
 def test_run_gpu_matches_cpu(ft, example, tmp_path):
-    # in this process: a process that has made cooperative launches keeps
-    # the GPU's cooperative-launch resource, so a child process could not
+    # the harness's functions in this process (the command line tool has
+    # its own test)
     import run_trie_search
     outs = {}
     for dev in ("gpu", "cpu"):
