@@ -12,7 +12,8 @@
 
 namespace ftk {  // the device side is not linked here
 hipError_t launch_tbs(const KArgs&, hipStream_t) { return hipErrorUnknown; }
-hipError_t clear_controls(uint8_t*, uint64_t, uint64_t, uint32_t, hipStream_t) {
+hipError_t clear_controls(uint8_t*, uint64_t, uint64_t, uint64_t, uint32_t, uint32_t,
+                          hipStream_t) {
   return hipErrorUnknown;
 }
 hipError_t scratch_address(int, void**) { return hipErrorUnknown; }
