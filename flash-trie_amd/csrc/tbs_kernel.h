@@ -62,10 +62,16 @@ struct SelRec {     // a push into `selected`
   uint32_t isnew;   // pushed during the current step
 };
 
+// History record of a hypothesis kept in a beam: its last token and its
+// parent's, the parent's record and the grandparent's, so that a result's
+// tokens are read back two per dependent load.
 struct HistRec {
-  uint32_t phist;
-  uint32_t tok;
+  uint32_t phist;   // the parent's record (kNoHist: the parent is the root)
+  uint32_t tok;     // the hypothesis's last token
+  uint32_t ptok;    // the parent's last token (when phist != kNoHist)
+  uint32_t phist2;  // the grandparent's record (when phist != kNoHist)
 };
+static_assert(sizeof(HistRec) == 16, "HistRec layout");
 
 struct OutHeader {  // 64 bytes, then norms[F] f64, lengths[F], tokens[F*T]
   uint32_t count;

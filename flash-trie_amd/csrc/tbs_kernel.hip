@@ -1157,6 +1157,14 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
       if ((v >> 32) == a.epoch && (uint32_t)v != kGoExit && v != seen) {
         // the step's parameters, read once after `go` and shared through LDS
         // so that every thread takes the same branches below
+        // Take this workgroup's slice of the step: its claim word is raised
+        // to this step's (epoch, generation) unless it already holds it or
+        // a later one -- the leader took the slice over first.  The claim
+        // goes out with the reads of the step's parameters; a successful
+        // one also proves they are this step's: the leader writes the next
+        // step's only after every claimed slice is done.
+        unsigned long long* cl = (unsigned long long*)(ws + a.lay.claims) + g;
+        const bool claimed = !a.no_claims && atomicMax(cl, v) < v;
         const uint32_t pt = ld_relaxed(&ctl->t), pW = ld_relaxed(&ctl->W),
                        pn = ld_relaxed(&ctl->n_par), pS = ld_relaxed(&ctl->nS);
         sm.hstep[0] = pt;
@@ -1165,30 +1173,27 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
         sm.hstep[3] = pS;
         sm.hstep[4] = ld_relaxed(&ctl->cur_which);
         sm.hstep[5] = ld_relaxed(&ctl->sel_which);
-        // Take this workgroup's slice of the step: its claim word goes from
-        // an older (epoch, generation) to this one, unless the leader took
-        // the slice over first (the word already holds this step or a
-        // later one).  A successful claim also proves the parameters just
-        // read are this step's: the leader writes the next step's only
-        // after every claimed slice is done.  A posted step always
-        // satisfies the bounds below; anything else is not taken.
+        // A posted step always satisfies the bounds below; a claimed slice
+        // of anything else is counted done without being expanded.
         const uint64_t max_w = (uint64_t)pn * max(a.scan_limit, d.K);
         const bool sane = pt < d.T && pn != 0 && pn <= a.lay.cur_cap &&
                           pS <= a.lay.sel_cap && (uint64_t)pW <= max_w;
-        unsigned long long* cl = (unsigned long long*)(ws + a.lay.claims) + g;
-        const unsigned long long c = ld_relaxed(cl);
-        if (sane && !a.no_claims && c < v && atomicCAS(cl, c, v) == c) sm.hstep[6] = 1;
+        sm.hstep[6] = claimed ? (sane ? 1u : 2u) : 0u;
       }
     }
     __syncthreads();
     const unsigned long long v = sm.bcast;
     const uint32_t t = sm.hstep[0], W = sm.hstep[1], n_par = sm.hstep[2],
                    nS = sm.hstep[3], cur_which = sm.hstep[4], sel_which = sm.hstep[5];
-    const bool mine = sm.hstep[6] != 0;
+    const uint32_t mine = sm.hstep[6];
     __syncthreads();
     if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
     seen = v;
-    if (!mine) continue;  // the leader took this slice over
+    if (mine == 0) continue;  // the leader took this slice over
+    if (mine == 2) {          // (never for a posted step)
+      if (tid == 0) atomicAdd(&ctl->done, 1u);
+      continue;
+    }
     StepView sv;
     sv.cur = (const CurRec*)(ws + (cur_which ? a.lay.cur1 : a.lay.cur0));
     sv.sel = (SelRec*)(ws + (sel_which ? a.lay.selB : a.lay.selA));
@@ -1302,6 +1307,9 @@ __device__ __forceinline__ void tiny_steps(
   // this lane's hypothesis
   bool alive = lane < n_cur;
   uint32_t node = 0, hst = kNoHist, mode = M_LP_NEXT, sd = 0, ptok = 0, tc = kNoCursor;
+  // the hypothesis's own history record: its last token and its parent's
+  // record, the links of the record a step below adds
+  uint32_t rtok = 0, rphist = kNoHist;
   double s = 0.0;
   if (alive) {
     node = sm.p_node[lane];
@@ -1311,6 +1319,11 @@ __device__ __forceinline__ void tiny_steps(
     sd = sm.p_c0[lane];
     ptok = sm.p_aux[lane];
     tc = sm.p_lp[lane];
+    if (hst < a.lay.hist_cap) {
+      const HistRec r = hist[hst];
+      rtok = r.tok;
+      rphist = r.phist;
+    }
   }
   uint32_t status = 0;
   bool done = false;
@@ -1400,7 +1413,11 @@ __device__ __forceinline__ void tiny_steps(
       HistRec h;
       h.phist = hst;
       h.tok = ptok;
+      h.ptok = rtok;
+      h.phist2 = rphist;
       hist[o] = h;
+      rtok = ptok;
+      rphist = hst;
       hst = o;
       s = s2;
       // the pending token of step t + 1: on the node's own edge the next
@@ -1783,9 +1800,13 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       const unsigned long long mygo = tag | gen;
       unsigned long long* claims = (unsigned long long*)(ws + a.lay.claims);
       const uint32_t nh = a.wgs - 1;  // helper slots 1 .. nh (nh < kBlock)
+      bool pending_any = true;
       for (;;) {
         const int pending = __syncthreads_count(tid < nh && ld_relaxed(&claims[tid + 1]) != mygo);
-        if (pending == 0) break;
+        if (pending == 0) {
+          pending_any = false;
+          break;
+        }
         if (tid == 0) sm.lead_flag = (wall_clock64() - t_post > kGraceTicks) ? 1u : 0u;
         __syncthreads();
         const bool expired = sm.lead_flag != 0;
@@ -1793,18 +1814,19 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         if (expired) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (tid == 0) sm.n_stolen = 0;
-      __syncthreads();
-      if (tid < nh) {
-        unsigned long long* cl = &claims[tid + 1];
-        const unsigned long long c = ld_relaxed(cl);
-        if (c < mygo && atomicCAS(cl, c, mygo) == c) {
+      uint32_t n_stolen = 0;
+      if (pending_any) {
+        if (tid == 0) sm.n_stolen = 0;
+        __syncthreads();
+        // raise every unclaimed word: a slice whose word this raises is
+        // taken over here; one a helper raised first stays the helper's
+        if (tid < nh && atomicMax(&claims[tid + 1], mygo) < mygo) {
           const uint32_t k = atomicAdd(&sm.n_stolen, 1u);
           sm.stolen[k] = (uint16_t)(tid + 1);
         }
+        __syncthreads();
+        n_stolen = sm.n_stolen;
       }
-      __syncthreads();
-      const uint32_t n_stolen = sm.n_stolen;
       for (uint32_t i = 0; i < n_stolen; ++i) {
         const uint32_t slice = sm.stolen[i];
         __syncthreads();
@@ -2045,6 +2067,17 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       }
       const float x = row_ok ? sm.row_lp[q] : rlp[(uint64_t)t * K + q];
       const uint32_t tk = row_ok ? sm.row_id[q] : rid[(uint64_t)t * K + q];
+      // the parent's record gives the two links of the new one
+      HistRec h;
+      h.phist = phist;
+      h.tok = tk;
+      h.ptok = 0u;
+      h.phist2 = kNoHist;
+      if (phist < hist_cap) {
+        const HistRec pr = hist[phist];
+        h.ptok = pr.tok;
+        h.phist2 = pr.phist;
+      }
       ParEntry e{0u, 0u, (uint32_t)M_NONE, 0u, kNoCursor};
       uint32_t err = 0;
       if (next_table) {
@@ -2064,9 +2097,6 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       }
       const double s2 = ps + (double)x;
       st_cur(&cur2[o], s2, c.node, hist_used + o);
-      HistRec h;
-      h.phist = phist;
-      h.tok = tk;
       hist[hist_used + o] = h;
       if (next_table) {
         if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
@@ -2214,12 +2244,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         uint32_t* row = otok + (uint64_t)cntless * d.out_T;
         if (me.depth >= 1 && me.depth <= d.out_T) {
           row[me.depth - 1] = me.tok;
+          // each record holds its token and its parent's: two per load
           uint32_t h = me.phist;
-          for (int pos = (int)me.depth - 2; pos >= 0; --pos) {
+          for (int pos = (int)me.depth - 2; pos >= 0; pos -= 2) {
             if (h >= hist_cap) break;
             const HistRec hr = hist[h];
             row[pos] = hr.tok;
-            h = hr.phist;
+            if (pos >= 1) row[pos - 1] = hr.ptok;
+            h = hr.phist2;
           }
         }
       }

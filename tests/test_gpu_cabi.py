@@ -58,7 +58,7 @@ def test_second_process_searches_after_this_one(ft, tmp_path):
     t.build([[1, 2, 3, 4], [1, 2, 3, 5], [7]])
     t.init_tbs_gpu(1, max_num_topk=8, max_num_outpos=4, max_num_out_beams=8,
                    max_num_out_tokens=32, max_num_inter_beams=64)
-    got = ft.bs_tbs_gpu(t, 1, [[10] * 4], [[[1, 2, 3, 4, 5, 7]] * 4],
+    got = ft.bs_tbs_gpu(t, 1, [[8] * 4], [[[1, 2, 3, 4, 5, 7]] * 4],
                         [[[-0.5, -3, -3, -3, -3, -1.0]] * 4], -10.0, -40.0, 0.0, False)
     assert got[0][0]
     write_dataset(ft, str(tmp_path))
