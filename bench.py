@@ -99,7 +99,23 @@ def parse():
                    help="also time the oracle's as-written cost model on one "
                         "request (minutes at the paper trie's 2.2M-child root)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--child-index", default="records", choices=["records", "louds"],
+                   help="child ranges from the node records or from the LOUDS "
+                        "rank/select directory")
     return p.parse_args()
+
+
+def device_free_bytes():
+    """Free device memory (hipMemGetInfo on the current device), or None."""
+    import ctypes
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+    except OSError:
+        return None
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    if hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) != 0:
+        return None
+    return free.value
 
 
 def kernel_hash():
@@ -289,11 +305,20 @@ def main():
     widths = [int(x) for x in args.beam_sweep.split(",") if x.strip()]
     widths = [w for w in widths if w < B] if args.config == "paper" else []
     t0 = time.time()
+    if args.child_index == "louds":
+        os.environ["FT_CHILD_INDEX"] = "louds"
+    free0 = device_free_bytes()
     trie.init_tbs_gpu(max(batches), max_num_topk=B, max_num_outpos=T,
                       max_num_out_beams=B, max_num_out_tokens=B * T,
                       max_num_inter_beams=B * T)
+    free1 = device_free_bytes()
     info = trie.device_info()
-    log(f"device {info}; context ready in {time.time() - t0:.1f}s")
+    # device memory of the context: image, labels, wide-node tables (and the
+    # LOUDS directory when chosen), workspace and staging
+    dev_bytes = (free0 - free1) if free0 is not None and free1 is not None else None
+    log(f"device {info}; context ready in {time.time() - t0:.1f}s; "
+        f"{(dev_bytes or 0) / 2**30:.2f} GiB of device memory "
+        f"(image {trie.total_size() / 2**30:.2f} GiB)")
 
     # ---- the boundary protocol, per proposal model ------------------------
     boundary, reqsets, hashsets = {}, {}, {}
@@ -340,25 +365,31 @@ def main():
         log(f"device-resident batch {b}: {dev_qps[b]:.0f} q/s, kernel mean "
             f"{kern_ms[b].mean():.3f} ms p99 {np.percentile(kern_ms[b], 99):.3f} ms")
     dev_peak = max(dev_qps, key=dev_qps.get)
-    mb = max(batches)
-    used = P - P % mb
-    for first in range(0, used, mb):
-        ft.launch(trie, first, mb)
-    if used < P:
-        ft.launch(trie, used, P - used)
-    ft.sync(trie)
-    cnt, norms, lens, toks, timing = ft.fetch(trie)
-    dev = timing["device_ms"]
-    phase = {"expand_ms": float(dev[:, 0].mean()), "select_ms": float(dev[:, 1].mean()),
-             "other_ms": float(dev[:, 2].mean()), "device_total_ms": float(dev[:, 3].mean())}
-    ss = timing["step_stats"].astype(np.float64)
     tick_ms = 1.0 / info["wall_clock_khz"]
-    log("per step (mean over the pool): parents, work, next, sel, expand_ms, "
-        "select_ms, children, probes")
-    for t in range(ss.shape[1]):
-        m = ss[:, t, :].mean(axis=0)
-        log(f"  step {t:2d}: {m[0]:7.1f} {m[1]:9.1f} {m[2]:7.1f} {m[3]:6.1f} "
-            f"{m[4] * tick_ms:7.4f} {m[5] * tick_ms:7.4f} {m[6]:9.1f} {m[7]:9.1f}")
+    # per-step device profile of the pool, searched at batch 1 and at the
+    # largest batch (the fetch after the largest batch keeps its results)
+    phase = {}
+    for pb in sorted({1, max(batches)}):
+        used = P - P % pb
+        for first in range(0, used, pb):
+            ft.launch(trie, first, pb)
+        if used < P:
+            ft.launch(trie, used, P - used)
+        ft.sync(trie)
+        cnt, norms, lens, toks, timing = ft.fetch(trie)
+        dev = timing["device_ms"]
+        phase[str(pb)] = {"expand_ms": float(dev[:, 0].mean()),
+                          "select_ms": float(dev[:, 1].mean()),
+                          "other_ms": float(dev[:, 2].mean()),
+                          "device_total_ms": float(dev[:, 3].mean())}
+        ss = timing["step_stats"].astype(np.float64)
+        log(f"per step at batch {pb} (mean over the pool): parents, work, next, "
+            "sel, expand_ms, select_ms, children, probes")
+        for t in range(ss.shape[1]):
+            m = ss[:, t, :].mean(axis=0)
+            log(f"  step {t:2d}: {m[0]:7.1f} {m[1]:9.1f} {m[2]:7.1f} {m[3]:6.1f} "
+                f"{m[4] * tick_ms:7.4f} {m[5] * tick_ms:7.4f} {m[6]:9.1f} {m[7]:9.1f}")
+        log(f"phases per request at batch {pb} (ms): {phase[str(pb)]}")
 
     # ---- other beam widths at the boundary ----------------------------------
     for w in widths:
@@ -515,6 +546,8 @@ def main():
         "workload_stats": wstats,
         "parity": parity,
         "device": info,
+        "memory": {"image_bytes": trie.total_size(), "context_device_bytes": dev_bytes,
+                   "child_index": args.child_index},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

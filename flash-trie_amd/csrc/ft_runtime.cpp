@@ -85,6 +85,11 @@ struct ft_ctx {
   WideBucket* d_wtab = nullptr;
   uint64_t* d_wfp = nullptr;     // per bucket: slot fingerprints
   uint32_t* d_labels = nullptr;  // per node: first token | kSlotSel
+  // LOUDS child-range directory (FT_CHILD_INDEX=louds), else null
+  uint64_t* d_louds_words = nullptr;
+  uint32_t* d_louds_z = nullptr;
+  uint32_t* d_louds_s = nullptr;
+  uint64_t louds_bytes = 0;
   uint32_t wdir_log2 = 0, wide_min = 0;
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
 
@@ -330,6 +335,78 @@ static int build_labels(ft_ctx* c, const uint8_t* image) {
   return FT_OK;
 }
 
+// Builds the LOUDS directory of the trie's shape (tbs_kernel.h LoudsDir)
+// from the records' child ranges and uploads it: zero v at bit
+// child_begin(v + 1) + v - 1, every other bit of the 2N - 1 a one; zeros
+// before every 512-bit block; the block of every kLoudsSel-th zero.
+static int build_louds(ft_ctx* c, const uint8_t* image) {
+  const uint64_t N = c->hdr.num_nodes;
+  const ft_node_rec* R = (const ft_node_rec*)(image + c->hdr.recs_offset);
+  const uint64_t nbits = 2 * N - 1;
+  const uint64_t wpb = kLoudsBlockBits / 64;
+  const uint64_t nblocks = (nbits + kLoudsBlockBits - 1) / kLoudsBlockBits;
+  const uint64_t nwords = nblocks * wpb;
+  const uint64_t nsamp = (N - 1) / kLoudsSel + 2;
+  std::unique_ptr<uint64_t[]> W(new (std::nothrow) uint64_t[nwords]);
+  std::unique_ptr<uint32_t[]> Z(new (std::nothrow) uint32_t[nblocks + 1]);
+  std::unique_ptr<uint32_t[]> S(new (std::nothrow) uint32_t[nsamp]);
+  if (!W || !Z || !S) return fail(FT_E_NOMEM, "louds directory: host memory");
+  const int T = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  auto zpos = [&](uint64_t v) { return (uint64_t)R[v + 1].child_begin + v - 1; };
+  auto par = [&](uint64_t n, auto&& body) {
+    std::vector<std::thread> th;
+    for (int w = 0; w < T; ++w)
+      th.emplace_back([&, w]() { body(n * w / T, n * (w + 1) / T); });
+    for (auto& x : th) x.join();
+  };
+  // words: each thread owns a range of words and clears the zeros of the
+  // nodes whose zero falls in it (zpos is increasing in v: binary search)
+  par(nwords, [&](uint64_t w0, uint64_t w1) {
+    for (uint64_t w = w0; w < w1; ++w) W[w] = ~0ull;
+    uint64_t lo = 0, hi = N;  // first v with zpos(v) >= 64 * w0
+    while (lo < hi) {
+      const uint64_t mid = (lo + hi) / 2;
+      if (zpos(mid) < 64 * w0) lo = mid + 1; else hi = mid;
+    }
+    for (uint64_t v = lo; v < N; ++v) {
+      const uint64_t p = zpos(v);
+      if (p >= 64 * w1) break;
+      W[p >> 6] &= ~(1ull << (p & 63));
+    }
+  });
+  // zeros per block, then the exclusive prefix
+  par(nblocks, [&](uint64_t b0, uint64_t b1) {
+    for (uint64_t b = b0; b < b1; ++b) {
+      uint32_t z = 0;
+      for (uint64_t j = 0; j < wpb; ++j) {
+        const uint64_t base = (b * wpb + j) * 64;
+        uint64_t x = ~W[b * wpb + j];
+        if (base + 64 > nbits) x &= base >= nbits ? 0ull : ((1ull << (nbits - base)) - 1ull);
+        z += (uint32_t)__builtin_popcountll(x);
+      }
+      Z[b + 1] = z;
+    }
+  });
+  Z[0] = 0;
+  for (uint64_t b = 1; b <= nblocks; ++b) Z[b] += Z[b - 1];
+  if (Z[nblocks] != N) return fail(FT_E_IMAGE, "louds directory: zero count mismatch");
+  for (uint64_t k = 0; k < nsamp; ++k)
+    S[k] = (uint32_t)(zpos(std::min<uint64_t>(k * kLoudsSel, N - 1)) / kLoudsBlockBits);
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_louds_words, nwords * 8)) != hipSuccess)
+    return hip_fail(e, "hipMalloc(louds words)");
+  if ((e = hipMalloc(&c->d_louds_z, (nblocks + 1) * 4)) != hipSuccess)
+    return hip_fail(e, "hipMalloc(louds z)");
+  if ((e = hipMalloc(&c->d_louds_s, nsamp * 4)) != hipSuccess)
+    return hip_fail(e, "hipMalloc(louds samples)");
+  if ((e = hipMemcpy(c->d_louds_words, W.get(), nwords * 8, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(c->d_louds_z, Z.get(), (nblocks + 1) * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(c->d_louds_s, S.get(), nsamp * 4, hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(e, "hipMemcpy(louds)");
+  c->louds_bytes = nwords * 8 + (nblocks + 1) * 4 + nsamp * 4;
+  return FT_OK;
+}
+
 // Builds the wide-node index on the host (parallel) and uploads it.
 static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   const char* env = std::getenv("FT_WIDE_MIN");
@@ -568,6 +645,14 @@ int ft_create(const void* image, size_t image_bytes, int device,
   if (int rc = build_wide_index(c, (const uint8_t*)image)) {
     ft_destroy(c);
     return rc;
+  }
+  if (const char* ci = std::getenv("FT_CHILD_INDEX")) {
+    if (std::strcmp(ci, "louds") == 0) {
+      if (int rc = build_louds(c, (const uint8_t*)image)) {
+        ft_destroy(c);
+        return rc;
+      }
+    }
   }
   c->max_resident = tbs_max_resident_blocks(c->num_cus);
   if (c->max_resident <= 0) {
@@ -1026,6 +1111,9 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
   a.no_claims = c->no_claims;
+  a.louds_words = c->d_louds_words;
+  a.louds_z = c->d_louds_z;
+  a.louds_s = c->d_louds_s;
   return a;
 }
 
@@ -1304,6 +1392,9 @@ void ft_destroy(ft_ctx* c) {
   if (c->d_wtab) (void)hipFree(c->d_wtab);
   if (c->d_wfp) (void)hipFree(c->d_wfp);
   if (c->d_labels) (void)hipFree(c->d_labels);
+  if (c->d_louds_words) (void)hipFree(c->d_louds_words);
+  if (c->d_louds_z) (void)hipFree(c->d_louds_z);
+  if (c->d_louds_s) (void)hipFree(c->d_louds_s);
   for (auto& ev : c->ring)
     if (ev) (void)hipEventDestroy(ev);
   if (c->stage_ev) (void)hipEventDestroy(c->stage_ev);

@@ -213,7 +213,25 @@ struct KArgs {
   // helpers never claim their slices (a test of the leader's take-over of
   // unclaimed slices; never set otherwise)
   uint32_t no_claims;
+  uint32_t pad1;
+  // Child ranges from the LOUDS rank/select directory instead of the node
+  // records' child_begin (null: records), see LoudsDir.
+  const uint64_t* louds_words;  // the LOUDS bits, 64 a word
+  const uint32_t* louds_z;      // zeros before each 512-bit block
+  const uint32_t* louds_s;      // block of every kLoudsSel-th zero
 };
+
+// LOUDS directory of the trie's shape: for every node v in breadth-first
+// order, deg(v) one bits then one zero bit, so zero v sits at bit
+// child_begin(v + 1) + v - 1 and node v's children are the ids
+// [select0(v - 1) - v + 2, select0(v) - v + 1) (select0(-1) = -1).
+// select0(i): the sample louds_s[i / kLoudsSel] and the next one bound the
+// 512-bit block holding zero i; the block is found among them by binary
+// search of louds_z (zeros before each block), and the zero within the
+// block's 8 words by popcounts.  2 bits per node plus 1/64 of that for
+// louds_z and ~1/128 for louds_s.
+constexpr uint32_t kLoudsSel = 256;
+constexpr uint32_t kLoudsBlockBits = 512;
 
 // Launches the search over `batch` requests (wgs workgroups each) on
 // `stream` (an ordinary launch: no workgroup waits for one that may not be

@@ -644,6 +644,59 @@ __device__ __forceinline__ Bound bounded_select(uint32_t n, uint32_t M, GetKey k
   return b;
 }
 
+// Position of the i-th zero bit (0-based) of the LOUDS bits (see LoudsDir).
+__device__ __forceinline__ uint64_t louds_select0(const KArgs& a, uint32_t i) {
+  const uint32_t k = i / kLoudsSel;
+  uint32_t lo = a.louds_s[k], hi = a.louds_s[k + 1];
+  // the last block b in [lo, hi] with louds_z[b] <= i
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) >> 1;
+    if (a.louds_z[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  uint32_t r = i - a.louds_z[lo];
+  const uint4* line = (const uint4*)(a.louds_words + (uint64_t)lo * (kLoudsBlockBits / 64));
+  const uint4 q0 = line[0], q1 = line[1], q2 = line[2], q3 = line[3];
+  const uint64_t w[8] = {(uint64_t)q0.x | ((uint64_t)q0.y << 32), (uint64_t)q0.z | ((uint64_t)q0.w << 32),
+                         (uint64_t)q1.x | ((uint64_t)q1.y << 32), (uint64_t)q1.z | ((uint64_t)q1.w << 32),
+                         (uint64_t)q2.x | ((uint64_t)q2.y << 32), (uint64_t)q2.z | ((uint64_t)q2.w << 32),
+                         (uint64_t)q3.x | ((uint64_t)q3.y << 32), (uint64_t)q3.z | ((uint64_t)q3.w << 32)};
+  // the word holding it: walk the words while r is past their zeros (the
+  // block holds zero i, so the walk stops inside it)
+  uint32_t wi = 0;
+  uint64_t z = ~w[0];
+#pragma unroll
+  for (int j = 0; j < 7; ++j) {
+    const uint32_t c = (uint32_t)__popcll(~w[j]);
+    if (wi == (uint32_t)j && r >= c) {
+      r -= c;
+      wi = j + 1;
+      z = ~w[j + 1];
+    }
+  }
+  // the r-th set bit of z, by halving
+  uint32_t pos = 0;
+#pragma unroll
+  for (int width = 32; width >= 1; width >>= 1) {
+    const uint64_t low = width == 64 ? ~0ull : ((1ull << width) - 1ull);
+    const uint32_t c = (uint32_t)__popcll(z & low);
+    if (r >= c) {
+      r -= c;
+      z >>= width;
+      pos += (uint32_t)width;
+    }
+  }
+  return (uint64_t)lo * kLoudsBlockBits + (uint64_t)wi * 64u + pos;
+}
+
+// First child id and degree of `node` from the LOUDS directory.
+__device__ __forceinline__ void louds_children(const KArgs& a, uint32_t node, uint32_t* c0,
+                                               uint32_t* deg) {
+  const uint64_t z1 = louds_select0(a, node);
+  const uint64_t z0 = node ? louds_select0(a, node - 1) : ~0ull;  // select0(-1) = -1
+  *c0 = (uint32_t)(z0 + 2u - node);
+  *deg = (uint32_t)(z1 - z0 - 1u);
+}
+
 // KB(n)[j] for a link parent: walk up until the edge that covers position j.
 __device__ __forceinline__ uint32_t kb_token(const KArgs& a, uint32_t n, ft_node_rec r,
                              uint32_t j, uint32_t* err) {
@@ -673,13 +726,19 @@ constexpr uint32_t kNoToken = 0xFFFFFFFFu;
 struct ParEntry {
   uint32_t c0, aux, mode, work, lp;
 };
+template <bool kLouds>
 __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, uint32_t t,
                                                  uint32_t K, uint32_t* err) {
   const ft_node_rec r = a.recs[node];
-  const uint32_t cend = a.recs[node + 1].child_begin;
-  const uint32_t deg = cend - r.child_begin;
+  uint32_t c0, deg;
+  if constexpr (kLouds) {
+    louds_children(a, node, &c0, &deg);
+  } else {
+    c0 = r.child_begin;
+    deg = a.recs[node + 1].child_begin - c0;
+  }
   const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
-  ParEntry e{r.child_begin, deg, (uint32_t)M_NONE, 0u, kNoCursor};
+  ParEntry e{c0, deg, (uint32_t)M_NONE, 0u, kNoCursor};
   if ((r.meta & FT_META_TERMINAL) && sd > t) {
     // link parent: only KB(n)[|Q|] extends it (louds-trie.cc:91-102)
     e.aux = kb_token(a, node, r, t, err);
@@ -1491,6 +1550,10 @@ __device__ __forceinline__ void tiny_steps(
   }
 }
 
+// kLouds: child ranges from the LOUDS directory (KArgs::louds_*) instead
+// of the node records -- a separate instantiation, so that the records'
+// kernel keeps its own register allocation.
+template <bool kLouds>
 __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   __shared__ Smem sm;
   // request-major interleave: request r owns blocks r, r + batch, ...  The
@@ -1573,7 +1636,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   }
   uint32_t root_err = 0;
   if (tid == 64u) {
-    const ParEntry e = parent_entry(a, 0u, 0u, K, &root_err);
+    const ParEntry e = parent_entry<kLouds>(a, 0u, 0u, K, &root_err);
     st_dev(&par_c0[0], e.c0);
     st_dev(&par_aux[0], e.aux);
     st_dev(&par_node[0], 0u);
@@ -1665,7 +1728,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       }
       const CurRec p = cur[j];
       uint32_t err = 0;
-      const ParEntry e = parent_entry(a, p.node, t, K, &err);
+      const ParEntry e = parent_entry<kLouds>(a, p.node, t, K, &err);
       if (err) atomicOr(&sm.status, (uint32_t)kStatusCorrupt);
       st_dev(&par_c0[j], e.c0);
       st_dev(&par_aux[j], e.aux);
@@ -2092,7 +2155,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
           e.work = 1;
           e.lp = sm.x_tc[j] + 1u;
         } else {
-          e = parent_entry(a, c.node, t + 1, K, &err);
+          e = parent_entry<kLouds>(a, c.node, t + 1, K, &err);
         }
       }
       const double s2 = ps + (double)x;
@@ -2328,7 +2391,12 @@ hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64
 // and the leader takes over the slices no helper has claimed), so the grid
 // needs no co-residency guarantee.
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
-  hipLaunchKernelGGL(tbs_kernel, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream, args);
+  if (args.louds_words)
+    hipLaunchKernelGGL(tbs_kernel<true>, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream,
+                       args);
+  else
+    hipLaunchKernelGGL(tbs_kernel<false>, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream,
+                       args);
   return hipGetLastError();
 }
 
@@ -2336,7 +2404,7 @@ int tbs_block_threads() { return kBlock; }
 
 int tbs_max_resident_blocks(int num_cus) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)tbs_kernel,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)tbs_kernel<false>,
                                                    kBlock, 0) != hipSuccess)
     return 0;
   return per_cu * num_cus;

@@ -426,3 +426,49 @@ def test_stress_long_keys_tight_thresholds(ft, po, early):
             assert_same_results((got[0][i], got[1][i]), want,
                                 f"stress req {b0 + i} early={early}")
         assert any(len(s) for s in got[0]), "every stress request came back empty"
+
+
+def test_louds_child_index(ft, po, monkeypatch):
+    # child ranges from the LOUDS rank/select directory (FT_CHILD_INDEX=louds)
+    # instead of the node records: tiny random tries, a 50k-key trie in
+    # batches, and a 6000-way root (zeros far apart around its run of ones)
+    monkeypatch.setenv("FT_CHILD_INDEX", "louds")
+    rng = np.random.default_rng(17)
+    for case in range(40):
+        vocab = int(rng.integers(2, 10))
+        keys = sorted({tuple(rng.integers(0, vocab, int(rng.integers(1, 7))))
+                       for _ in range(int(rng.integers(1, 40)))})
+        keys = [list(map(int, k)) for k in keys]
+        T, K = int(rng.integers(1, 8)), int(rng.integers(1, vocab + 1))
+        ids = np.stack([np.sort(rng.choice(vocab, K, replace=False))
+                        for _ in range(T)]).astype(np.uint32)
+        lp = (-rng.integers(0, 8, (T, K)) * 0.5).astype(np.float32)
+        beams = [int(rng.integers(1, 6)) for _ in range(T)]
+        t = _gpu_trie(ft, keys=keys, batch=1, topk=16, steps=8, beams=8)
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids.tolist()], [lp.tolist()],
+                            -3.0, -9.0, 5.0, False)
+        want = po.OracleTrie.from_keys(keys).tbs(beams, ids, lp, -3.0, -9.0, 5.0, False)
+        assert_same_results((got[0][0], got[1][0]), want, f"louds tiny {case}")
+    toks, offs = ft.synth_keys(50000, 4096, 3, 8, 1.1, 4)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=32, steps=8, beams=16,
+                  inter=2048)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 16, 4096, 8, 32, 16, 0.3, 2.0, True, 4, model=1)
+    for b0 in range(0, 16, 4):
+        got = ft.bs_tbs_gpu(t, 4, [[16] * 8] * 4, [ids[b0 + i].tolist() for i in range(4)],
+                            [lp[b0 + i].tolist() for i in range(4)], -10.0, -40.0, 5.0, False)
+        for i in range(4):
+            want = o.tbs([16] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, False)
+            assert_same_results((got[0][i], got[1][i]), want, f"louds 50k {b0 + i}")
+    keys = []
+    for k in range(6000):
+        keys += [[k], [k, k % 3], [k, 1000 + k % 5, k % 7]]
+    t = _gpu_trie(ft, keys=keys, batch=1, topk=4096, steps=3, beams=3000, inter=16384)
+    o = po.OracleTrie.from_keys(keys)
+    ids = np.stack([np.sort(rng.choice(6000, 4096, replace=False)),
+                    np.arange(4096), np.arange(4096)]).astype(np.uint32)
+    lp = np.array([-0.5, -1.0, -2.0], dtype=np.float32)[rng.choice(3, (3, 4096))]
+    got = ft.bs_tbs_gpu(t, 1, [[2500, 3000, 40]], [ids.tolist()], [lp.tolist()],
+                        -10.0, -40.0, 5.0, False)
+    want = o.tbs([2500, 3000, 40], ids, lp, -10.0, -40.0, 5.0, False)
+    assert_same_results((got[0][0], got[1][0]), want, "louds wide root")
