@@ -370,6 +370,7 @@ def main():
     # largest batch (the fetch after the largest batch keeps its results)
     phase = {}
     for pb in sorted({1, max(batches)}):
+        ft.launch(trie, 0, min(3, P))  # a separator in kernel traces
         used = P - P % pb
         for first in range(0, used, pb):
             ft.launch(trie, first, pb)
@@ -384,11 +385,19 @@ def main():
                           "device_total_ms": float(dev[:, 3].mean())}
         ss = timing["step_stats"].astype(np.float64)
         log(f"per step at batch {pb} (mean over the pool): parents, work, next, "
-            "sel, expand_ms, select_ms, children, probes")
+            "sel, expand_ms, select_ms, children, probes, claim_wait_ms, "
+            "done_wait_ms")
+        steps_tab = []
         for t in range(ss.shape[1]):
             m = ss[:, t, :].mean(axis=0)
+            steps_tab.append([round(float(x), 1) for x in m[:4]] +
+                             [round(float(x * tick_ms), 4) for x in (m[4], m[5])] +
+                             [round(float(x), 1) for x in m[6:8]] +
+                             [round(float(x * tick_ms), 4) for x in m[8:10]])
             log(f"  step {t:2d}: {m[0]:7.1f} {m[1]:9.1f} {m[2]:7.1f} {m[3]:6.1f} "
-                f"{m[4] * tick_ms:7.4f} {m[5] * tick_ms:7.4f} {m[6]:9.1f} {m[7]:9.1f}")
+                f"{m[4] * tick_ms:7.4f} {m[5] * tick_ms:7.4f} {m[6]:9.1f} {m[7]:9.1f} "
+                f"{m[8] * tick_ms:7.4f} {m[9] * tick_ms:7.4f}")
+        phase[str(pb)]["steps"] = steps_tab
         log(f"phases per request at batch {pb} (ms): {phase[str(pb)]}")
 
     # ---- other beam widths at the boundary ----------------------------------

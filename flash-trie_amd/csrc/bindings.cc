@@ -32,6 +32,8 @@
 #include "trie_impl.h"
 
 namespace py = pybind11;
+// u64 per step of ft_result::step_stats (include/flashtrie_amd.h)
+constexpr size_t ftk_step_stats = FT_STEP_STATS;
 using marisa::Label;
 using marisa::TbsInput;
 using marisa::Trie;
@@ -454,8 +456,8 @@ PYBIND11_MODULE(flashtrie, m) {
     py::array_t<uint32_t> lens({(py::ssize_t)B, (py::ssize_t)Fm});
     py::array_t<uint32_t> toks({(py::ssize_t)B, (py::ssize_t)Fm, (py::ssize_t)Tm});
     py::array_t<double> dev({(py::ssize_t)B, (py::ssize_t)4});
-    py::array_t<uint64_t> steps({(py::ssize_t)B, (py::ssize_t)Tm, (py::ssize_t)8});
-    std::memset(steps.mutable_data(), 0, B * Tm * 8 * 8);
+    py::array_t<uint64_t> steps({(py::ssize_t)B, (py::ssize_t)Tm, (py::ssize_t)ftk_step_stats});
+    std::memset(steps.mutable_data(), 0, B * Tm * ftk_step_stats * 8);
     std::memset(norms.mutable_data(), 0, B * Fm * 8);
     std::memset(lens.mutable_data(), 0, B * Fm * 4);
     std::memset(toks.mutable_data(), 0, B * Fm * Tm * 4);
@@ -467,7 +469,7 @@ PYBIND11_MODULE(flashtrie, m) {
       res[b].logp_norm = norms.mutable_data() + b * Fm;
       res[b].length = lens.mutable_data() + b * Fm;
       res[b].tokens = toks.mutable_data() + b * Fm * Tm;
-      res[b].step_stats = steps.mutable_data() + b * Tm * 8;
+      res[b].step_stats = steps.mutable_data() + b * Tm * ftk_step_stats;
     }
     ft_timing tm{};
     int rc;

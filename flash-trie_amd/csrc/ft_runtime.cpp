@@ -29,6 +29,7 @@
 using namespace ftk;
 
 static_assert(kScratchBytes == FT_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");
+static_assert(kStepStats == FT_STEP_STATS, "the header states the per-step profile");
 
 namespace {
 

@@ -83,8 +83,11 @@ static_assert(sizeof(OutHeader) == 64, "OutHeader layout");
 
 // Per-step profile written after the output tokens of each request:
 // parents, work items, next pushes, selected pushes, expansion ticks,
-// selection ticks, child records scanned, binary-search probes.
-constexpr uint32_t kStepStats = 8;
+// selection ticks, child records scanned, binary-search probes, and for a
+// shared step the leader's waits after its own slice: for the helpers'
+// claims (and its take-over of unclaimed slices) and for the claimed
+// slices to be done (wall-clock ticks).
+constexpr uint32_t kStepStats = 10;
 __host__ __device__ inline uint64_t step_stats_offset(uint32_t F, uint32_t T) {
   return (sizeof(OutHeader) + 12ull * F + 4ull * F * T + 7) & ~7ull;
 }

@@ -1860,6 +1860,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       // taken over here -- so the step never waits for a workgroup that is
       // not running.  Then every claimed slice is waited for: a helper that
       // claimed one is running and finishes it.
+      const unsigned long long tw0 = wall_clock64();
       const unsigned long long mygo = tag | gen;
       unsigned long long* claims = (unsigned long long*)(ws + a.lay.claims);
       const uint32_t nh = a.wgs - 1;  // helper slots 1 .. nh (nh < kBlock)
@@ -1904,12 +1905,18 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
                      hashed, sm);
       }
       if (tid == 0) {
+        const unsigned long long tw1 = wall_clock64();
         const uint32_t helped = nh - n_stolen;
         for (uint32_t it = 0; it < kSpinLimit; ++it) {
           if (ld_relaxed(&ctl->done) >= helped) break;
           __builtin_amdgcn_s_sleep(1);
         }
         if (ld_relaxed(&ctl->done) < helped) sm.status |= kStatusCorrupt;
+        if (t < d.out_T) {
+          uint64_t* row = step_stats + (uint64_t)t * kStepStats;
+          row[8] = tw1 - tw0;
+          row[9] = wall_clock64() - tw1;
+        }
       }
     }
     __syncthreads();

@@ -72,29 +72,41 @@ def run_summary(db, name_filter=""):
 
 
 def pmc_summary(db, name_filter="", runs=False):
+    """Mean counter value per dispatch, per (kernel, grid size) -- or, with
+    runs, per run of consecutive dispatches of one kernel and grid size
+    (a dispatch's counters are taken together, whatever their number)."""
     con = sqlite3.connect(db)
     rows = con.execute(
-        "select kernel_name, grid_size, workgroup_size, counter_name, value "
+        "select dispatch_id, kernel_name, grid_size, workgroup_size, counter_name, value "
         "from counters_collection order by dispatch_id").fetchall()
-    groups = {}
-    order = []
-    for name, grid, wg, counter, value in rows:
+    disp = {}
+    for did, name, grid, wg, counter, value in rows:
         if name_filter and name_filter not in name:
             continue
-        key = (name, grid // max(wg, 1), counter)
+        d = disp.setdefault(did, [(name, grid // max(wg, 1)), {}])
+        d[1][counter] = d[1].get(counter, 0.0) + value
+    groups = []  # [(key, {counter: [values]})]
+    index = {}
+    for did in sorted(disp):
+        key, vals = disp[did]
         if runs:
-            if not order or order[-1][0] != key:
-                order.append((key, []))
-            order[-1][1].append(value)
+            if not groups or groups[-1][0] != key:
+                groups.append((key, {}))
+            g = groups[-1][1]
         else:
-            groups.setdefault(key, []).append(value)
-    items = ([(k, v) for k, v in order] if runs else sorted(groups.items()))
+            if key not in index:
+                index[key] = len(groups)
+                groups.append((key, {}))
+            g = groups[index[key]][1]
+        for c, v in vals.items():
+            g.setdefault(c, []).append(v)
     out = []
-    for (name, wgs, counter), v in items:
-        v = np.array(v, dtype=np.float64)
-        out.append({"kernel": name, "workgroups": wgs, "counter": counter,
-                    "dispatches": v.size, "mean": v.mean(), "min": v.min(),
-                    "max": v.max()})
+    for (name, wgs), counters in groups:
+        for counter in sorted(counters):
+            v = np.array(counters[counter], dtype=np.float64)
+            out.append({"kernel": name, "workgroups": wgs, "counter": counter,
+                        "dispatches": v.size, "mean": v.mean(), "min": v.min(),
+                        "max": v.max()})
     return out
 
 

@@ -121,11 +121,16 @@ typedef struct ft_result {
   uint32_t* tokens;      /* [capacity * token_stride] */
   double device_ms[4];   /* out: expansion, selection, other, total (device
                             wall clock of this request's workgroup) */
-  uint64_t* step_stats;  /* optional [num_steps * 8]: per step parents, work
-                            items, next pushes, selected pushes, expansion
-                            and selection ticks (wall clock), child records
-                            scanned, binary-search probes */
+  uint64_t* step_stats;  /* optional [num_steps * FT_STEP_STATS]: per step
+                            parents, work items, next pushes, selected
+                            pushes, expansion and selection ticks (wall
+                            clock), child records scanned, binary-search
+                            probes, and for a step shared between
+                            workgroups the leader's wait for the helpers'
+                            claims and for their slices (ticks) */
 } ft_result;
+
+#define FT_STEP_STATS 10
 
 /* Per-launch timing and work counters (filled by ft_fetch when non-null). */
 typedef struct ft_timing {
