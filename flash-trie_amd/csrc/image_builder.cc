@@ -10,6 +10,11 @@
 // is level by level over the sorted keys (a group's edge only needs its
 // first and last key, and group boundaries are found by galloping search),
 // not the reference's queue-of-ranges walk.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include "image_builder.h"
 
 #include <algorithm>
@@ -31,9 +36,62 @@ static inline uint64_t align_up(uint64_t v, uint64_t a) {
 ImageBlob::~ImageBlob() { clear(); }
 
 void ImageBlob::clear() {
-  std::free(data_);
+  if (mapped_) {
+    if (data_) ::munmap(data_, size_);
+  } else {
+    std::free(data_);
+  }
   data_ = nullptr;
   size_ = 0;
+  mapped_ = false;
+}
+
+bool ImageBlob::read_file(const char* path, std::string* err) {
+  clear();
+  const int fd = ::open(path, O_RDONLY);
+  if (fd < 0) return *err = std::string("cannot open ") + path, false;
+  struct stat st;
+  if (::fstat(fd, &st) != 0) {
+    ::close(fd);
+    return *err = std::string("cannot stat ") + path, false;
+  }
+  const size_t n = (size_t)st.st_size;
+  data_ = (uint8_t*)std::aligned_alloc(256, ((n ? n : 1) + 255) / 256 * 256);
+  if (!data_) {
+    ::close(fd);
+    return *err = "out of host memory", false;
+  }
+  size_t got = 0;
+  while (got < n) {
+    const ssize_t r = ::read(fd, data_ + got, std::min<size_t>(n - got, 1u << 30));
+    if (r <= 0) {
+      ::close(fd);
+      clear();
+      return *err = std::string("read failed on ") + path, false;
+    }
+    got += (size_t)r;
+  }
+  ::close(fd);
+  size_ = n;
+  return true;
+}
+
+bool ImageBlob::map_file(const char* path, std::string* err) {
+  clear();
+  const int fd = ::open(path, O_RDONLY);
+  if (fd < 0) return *err = std::string("cannot open ") + path, false;
+  struct stat st;
+  if (::fstat(fd, &st) != 0 || st.st_size == 0) {
+    ::close(fd);
+    return *err = std::string("cannot map ") + path + " (empty or unreadable)", false;
+  }
+  void* p = ::mmap(nullptr, (size_t)st.st_size, PROT_READ | PROT_WRITE, MAP_PRIVATE, fd, 0);
+  ::close(fd);
+  if (p == MAP_FAILED) return *err = std::string("mmap failed on ") + path, false;
+  data_ = (uint8_t*)p;
+  size_ = (size_t)st.st_size;
+  mapped_ = true;
+  return true;
 }
 
 bool ImageBlob::allocate(uint64_t num_nodes, uint64_t tail_len) {

@@ -10,7 +10,8 @@
 
 namespace ftamd {
 
-// An owned, 256-byte aligned image blob.
+// An image blob: owned (256-byte aligned heap memory) or a private
+// read-write mapping of an image file (page aligned; writes stay private).
 class ImageBlob {
  public:
   ImageBlob() = default;
@@ -25,11 +26,18 @@ class ImageBlob {
   void swap(ImageBlob& o) noexcept {
     std::swap(data_, o.data_);
     std::swap(size_, o.size_);
+    std::swap(mapped_, o.mapped_);
   }
   // Allocates a zeroed blob laid out for the given sizes and fills the header.
   bool allocate(uint64_t num_nodes, uint64_t tail_len);
-  // Adopts a copy of an existing blob (e.g. read from a file).
+  // Adopts a copy of an existing blob.
   bool assign(const void* p, size_t n);
+  // Reads a whole file into a new blob (one read, no intermediate copy).
+  bool read_file(const char* path, std::string* err);
+  // Maps a whole file (private, copy-on-write): the pages are read on first
+  // use and shared with the page cache.
+  bool map_file(const char* path, std::string* err);
+  bool mapped() const { return mapped_; }
   void clear();
 
   bool empty() const { return data_ == nullptr; }
@@ -54,6 +62,7 @@ class ImageBlob {
  private:
   uint8_t* data_ = nullptr;
   size_t size_ = 0;
+  bool mapped_ = false;
 };
 
 // Builds the trie of `nkeys` keys (key i = toks[offs[i] .. offs[i+1])) with

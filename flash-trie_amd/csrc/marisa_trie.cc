@@ -234,31 +234,35 @@ void Trie::build(const std::vector<std::vector<Label>>& keys) {
   build(ks, 0);
 }
 
-void Trie::load(const char* filename) {
-  if (!filename) throw Exception(MARISA_NULL_ERROR, "load: null filename");
-  std::ifstream f(filename, std::ios::binary | std::ios::ate);
-  if (!f) throw Exception(MARISA_IO_ERROR, std::string("load: cannot open ") + filename);
-  const std::streamsize n = f.tellg();
-  f.seekg(0);
-  std::vector<uint64_t> buf(((size_t)n + 7) / 8);  // 8-byte aligned
-  if (n > 0 && !f.read((char*)buf.data(), n))
-    throw Exception(MARISA_IO_ERROR, std::string("load: read failed on ") + filename);
-  auto fresh = std::unique_ptr<TrieImpl>(new TrieImpl());
+namespace {
+
+// load (read the file) and mmap (map it): this library's image is used as
+// it is -- in place for a mapping -- and validated; a MARISA trie file
+// written by the reference (lib/marisa/trie.cc:21-53) is converted.
+void open_trie(const char* filename, bool map, std::unique_ptr<TrieImpl>* out) {
+  const char* who = map ? "mmap: " : "load: ";
+  if (!filename) throw Exception(MARISA_NULL_ERROR, std::string(who) + "null filename");
+  ftamd::ImageBlob file;
   std::string err;
-  if (ftamd::is_marisa_file(buf.data(), (size_t)n)) {
-    // a trie.bin written by the reference (lib/marisa/trie.cc:44-53)
-    if (!ftamd::image_from_marisa((const uint8_t*)buf.data(), (size_t)n, &fresh->img, &err))
-      throw Exception(MARISA_FORMAT_ERROR, std::string("load: ") + filename + ": " + err);
+  if (!(map ? file.map_file(filename, &err) : file.read_file(filename, &err)))
+    throw Exception(MARISA_IO_ERROR, who + err);
+  auto fresh = std::unique_ptr<TrieImpl>(new TrieImpl());
+  if (ftamd::is_marisa_file(file.data(), file.size())) {
+    if (!ftamd::image_from_marisa(file.data(), file.size(), &fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, std::string(who) + filename + ": " + err);
   } else {
-    if (!fresh->img.assign(buf.data(), (size_t)n))
-      throw Exception(MARISA_MEMORY_ERROR, "load: out of memory");
+    fresh->img.swap(file);
     if (!ftamd::validate_image(fresh->img, &err))
-      throw Exception(MARISA_FORMAT_ERROR, std::string("load: ") + err);
+      throw Exception(MARISA_FORMAT_ERROR, std::string(who) + err);
   }
-  impl_.swap(fresh);
+  out->swap(fresh);
 }
 
-void Trie::mmap(const char* filename) { load(filename); }
+}  // namespace
+
+void Trie::load(const char* filename) { open_trie(filename, false, &impl_); }
+
+void Trie::mmap(const char* filename) { open_trie(filename, true, &impl_); }
 
 void Trie::save(const char* filename) const {
   require_trie(impl_.get());

@@ -80,6 +80,44 @@ def test_save_load_roundtrip(ft, tmp_path):
     assert np.array_equal(t.image(), m.image())
 
 
+def test_mmap_maps_images_and_converts_marisa_files(ft, tmp_path):
+    # an image file is mapped and used in place; a MARISA trie file is
+    # converted from the mapping; both search like the built trie, and the
+    # mapping stays valid after the file is unlinked (the mapping holds it)
+    toks, offs = ft.synth_keys(3000, 512, 2, 6, 1.1, 5)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    p_img, p_bin = str(tmp_path / "trie.ftimg"), str(tmp_path / "trie.bin")
+    t.save(p_img)
+    t.save_marisa(p_bin)
+    ids, lp = ft.synth_requests(t, 0, 3, 512, 6, 16, 8, 0.3, 2.0, True, 5, model=1)
+    want = [ft.tbs(t, [8] * 6, ids[r].tolist(), lp[r].tolist(), -10.0, -40.0, 5.0, False)
+            for r in range(3)]
+    for path in (p_img, p_bin):
+        m = ft.Trie()
+        m.mmap(path)
+        if path == p_img:
+            import os
+            os.unlink(path)
+        if path == p_img:  # (a converted MARISA file keeps its shared tail)
+            assert np.array_equal(t.image(), m.image()), path
+        assert m.num_keys() == t.num_keys() and m.num_nodes() == t.num_nodes()
+        for r in range(3):
+            got = ft.tbs(m, [8] * 6, ids[r].tolist(), lp[r].tolist(), -10.0, -40.0, 5.0,
+                         False)
+            assert got[0] == want[r][0] and list(got[1]) == list(want[r][1])
+    with pytest.raises(RuntimeError):
+        ft.Trie().mmap(str(tmp_path / "missing.ftimg"))
+    empty = tmp_path / "empty.ftimg"
+    empty.write_bytes(b"")
+    with pytest.raises(RuntimeError):
+        ft.Trie().mmap(str(empty))
+    short = tmp_path / "short.ftimg"
+    short.write_bytes(t.image().tobytes()[:1000])
+    with pytest.raises(RuntimeError):
+        ft.Trie().mmap(str(short))
+
+
 def test_load_rejects_truncated_marisa_file(ft, tmp_path):
     # a MARISA header followed by too few bytes for its sections
     p = tmp_path / "trie.bin"
