@@ -118,9 +118,16 @@ def device_free_bytes():
     return free.value
 
 
-def kernel_hash():
-    with open(KERNEL_SRC, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()[:16]
+def kernel_hash(path=KERNEL_SRC):
+    """sha256 (first 16 hex digits) of the kernel source's code: // comments
+    and blank space removed, so that a comment edit keeps the stamp of the
+    profiles recorded on that code."""
+    code = []
+    for line in open(path, encoding="utf-8"):
+        line = re.sub(r"//.*$", "", line).strip()
+        if line:
+            code.append(re.sub(r"\s+", " ", line))
+    return hashlib.sha256("\n".join(code).encode()).hexdigest()[:16]
 
 
 def measured_traffic(cfg, batch):

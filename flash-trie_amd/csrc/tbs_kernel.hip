@@ -837,6 +837,21 @@ __device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
 // a reader issues its loads only after it has seen the signal.  The leader,
 // which re-reads the pushes many times during selection, instead invalidates
 // its caches once per step (an acquire fence) and then reads normally.
+//
+// What this rests on is the code LLVM generates for gfx942-class targets
+// (gfx950 included) from monotonic agent-scope atomics -- the "Memory Model
+// GFX942" table of LLVM's AMDGPUUsage: a load is `global_load ... sc1`, a
+// store `global_store ... sc1`, each served at the coherence point of the
+// agent rather than from a possibly stale non-coherent line; and on the
+// ordering the hardware gives a wave: memory operations issue in program
+// order, `s_waitcnt vmcnt(0)` returns only once every earlier store has
+// been acknowledged, and no load after a branch on a loaded value issues
+// before that value is back.  Under the C++ memory model alone relaxed
+// atomics would not order the data against the flag; release / acquire
+// would, but their agent-scope form writes back / invalidates the L2 of the
+// XCD (buffer_wbl2 sc1 / buffer_inv sc1), which measured ~50% of step-1
+// time when every helper did it every step.  The inline `s_waitcnt` below
+// carries a memory clobber, so the compiler keeps the stores before it.
 __device__ __forceinline__ unsigned long long ld_relaxed(const unsigned long long* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
