@@ -77,6 +77,13 @@ struct ft_ctx {
   uint64_t stage_cap = 0;
   uint8_t* d_stage = nullptr;
   uint8_t* h_stage = nullptr;
+  // the device's addresses of h_stage, h_out and h_ready (pinned, coherent
+  // host memory mapped for the device), read and written by the kernel in a
+  // streamed search
+  uint8_t* m_stage = nullptr;
+  uint8_t* m_out = nullptr;
+  unsigned long long* h_ready = nullptr;  // per staged request: ready word
+  unsigned long long* m_ready = nullptr;
 
   size_t max_staged = 0;  // staging / output capacity in requests
   uint64_t per_req = 0;   // staging bytes bound of one request
@@ -126,34 +133,53 @@ struct ft_ctx {
   uint64_t launches = 0;
 };
 
-static void release_workspace(ft_ctx* c) {
-  if (c->d_ws) (void)hipFree(c->d_ws);
+static void free_staging(ft_ctx* c) {
   if (c->d_out) (void)hipFree(c->d_out);
   if (c->d_stage) (void)hipFree(c->d_stage);
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->h_stage) (void)hipHostFree(c->h_stage);
-  c->d_ws = c->d_out = c->d_stage = c->h_out = c->h_stage = nullptr;
+  if (c->h_ready) (void)hipHostFree(c->h_ready);
+  c->d_out = c->d_stage = c->h_out = c->h_stage = c->m_stage = c->m_out = nullptr;
+  c->h_ready = c->m_ready = nullptr;
+  c->max_staged = 0;
+}
+
+static void release_workspace(ft_ctx* c) {
+  if (c->d_ws) (void)hipFree(c->d_ws);
+  c->d_ws = nullptr;
+  free_staging(c);
   c->reserved = false;
+}
+
+// Pinned, coherent host memory mapped for the device: *host for the host,
+// *dev for kernels.
+static int alloc_mapped(void** host, void** dev, size_t bytes, const char* what) {
+  hipError_t e = hipHostMalloc(host, bytes, hipHostMallocMapped | hipHostMallocCoherent);
+  if (e != hipSuccess) return *host = nullptr, hip_fail(e, what);
+  if ((e = hipHostGetDevicePointer(dev, *host, 0)) != hipSuccess) return hip_fail(e, what);
+  return FT_OK;
 }
 
 // (Re)allocates the staging and output buffers for n requests.
 static int alloc_staging(ft_ctx* c, size_t n) {
-  if (c->d_out) (void)hipFree(c->d_out);
-  if (c->d_stage) (void)hipFree(c->d_stage);
-  if (c->h_out) (void)hipHostFree(c->h_out);
-  if (c->h_stage) (void)hipHostFree(c->h_stage);
-  c->d_out = c->d_stage = c->h_out = c->h_stage = nullptr;
-  c->max_staged = 0;
+  free_staging(c);
   c->stage_cap = align_up(n * sizeof(DevReq), 256) + n * c->per_req;
   hipError_t e;
   if ((e = hipMalloc(&c->d_out, c->out_slot_max * n)) != hipSuccess)
     return hip_fail(e, "hipMalloc(output)");
   if ((e = hipMalloc(&c->d_stage, c->stage_cap)) != hipSuccess)
     return hip_fail(e, "hipMalloc(stage)");
-  if ((e = hipHostMalloc(&c->h_out, c->out_slot_max * n, 0)) != hipSuccess)
-    return hip_fail(e, "hipHostMalloc(output)");
-  if ((e = hipHostMalloc(&c->h_stage, c->stage_cap, 0)) != hipSuccess)
-    return hip_fail(e, "hipHostMalloc(stage)");
+  void *h = nullptr, *m = nullptr;
+  if (int rc = alloc_mapped(&h, &m, c->out_slot_max * n, "hipHostMalloc(output)")) return rc;
+  c->h_out = (uint8_t*)h;
+  c->m_out = (uint8_t*)m;
+  if (int rc = alloc_mapped(&h, &m, c->stage_cap, "hipHostMalloc(stage)")) return rc;
+  c->h_stage = (uint8_t*)h;
+  c->m_stage = (uint8_t*)m;
+  if (int rc = alloc_mapped(&h, &m, 8 * n, "hipHostMalloc(ready words)")) return rc;
+  c->h_ready = (unsigned long long*)h;
+  c->m_ready = (unsigned long long*)m;
+  std::memset(c->h_ready, 0, 8 * n);
   c->max_staged = n;
   return FT_OK;
 }
@@ -845,10 +871,13 @@ static RowScan scan_row(const uint32_t* rid, const float* rlp, uint32_t K, float
   return RowScan{bad, sorted, lo, hi};
 }
 
-// Packs one validated request into its block at `base` (see pack_batch):
-// the length-norm table, beam widths, token-sorted rows and per-step key
-// bounds.  Fails on NaN / +inf logps, duplicate token ids in a row and
-// non-finite length-norm factors.  `tmp` holds K pairs.
+// Packs one validated request into its block at `base` (see plan_batch):
+// the length-norm table, beam widths, per-step key bounds and token-sorted
+// rows, and sets d.rk_off / d.in_bytes: the proposals' indices in the
+// caller's rows are staged only when some row is out of order (else rk_off
+// is 0 and the index is the position), and in_bytes ends the block there.
+// Fails on NaN / +inf logps, duplicate token ids in a row and non-finite
+// length-norm factors.  `tmp` holds K pairs.
 static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
                         std::pair<uint32_t, uint32_t>* tmp, std::string* err) {
   auto who = [r]() { return "request " + std::to_string(r) + ": "; };
@@ -864,7 +893,10 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
   std::memcpy(base + d.beams_off, q.beams, 4ull * T);
   uint32_t* rid_s = (uint32_t*)(base + d.rid_off);
   float* rlp_s = (float*)(base + d.rlp_off);
-  uint16_t* rk_s = (uint16_t*)(base + d.rk_off);
+  // d.rk_off holds the planned offset of the indices until a row needs them
+  const uint32_t rk_planned = d.rk_off;
+  uint16_t* rk_s = (uint16_t*)(base + rk_planned);
+  bool rk_used = false;
   uint64_t* kb = (uint64_t*)(base + d.kb_off);
   // Per step, bounds of the keys pushed into `next`: a push's score is a
   // parent score plus a logp that passes the token threshold, and itself
@@ -886,8 +918,13 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
     const RowScan sc = scan_row(rid, rlp, K, q.token_logp_threshold, oid, olp);
     if (sc.bad) return *err = who() + "topk_logp holds NaN or +inf", FT_E_INPUT;
     if (sc.sorted) {
-      for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
+      if (rk_used)
+        for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
     } else {
+      if (!rk_used) {  // the rows before this one, in order: index = position
+        for (uint64_t i = 0; i < (uint64_t)t * K; ++i) rk_s[i] = (uint16_t)(i % K);
+        rk_used = true;
+      }
       for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
       std::sort(tmp, tmp + K);
       for (uint32_t p = 0; p < K; ++p) {
@@ -909,20 +946,21 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
     s_lo = lo;
     s_hi = hi;
   }
+  d.rk_off = rk_used ? rk_planned : 0u;
+  d.in_bytes = rk_used ? (uint32_t)align_up(rk_planned + 2ull * T * K, 16) : rk_planned;
   return FT_OK;
 }
 
-// Validates `batch` requests and packs them into H (cap bytes): DevReq[batch]
-// then each request's block (length-norm table, beam widths, token-sorted
-// rows, key bounds).  Fills staged[0, batch); *bytes = bytes used,
-// *out_stride = output bytes per request.  `tmp` holds max_topk pairs (the
-// buffer an unsorted row is sorted in).
-// An error names the first request (in batch order) that has one.
-// Allocates nothing on success.
-static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& lim,
-                      uint8_t* H, uint64_t cap, StagedReq* staged,
-                      std::pair<uint32_t, uint32_t>* tmp, uint64_t* bytes,
-                      uint64_t* out_stride) {
+// Checks the shapes of `batch` requests against the limits and lays them
+// out in H (cap bytes): DevReq[batch], then each request's block
+// (length-norm table, beam widths, key bounds, token-sorted rows, row
+// indices), without reading the rows.  Fills staged[0, batch) and the
+// DevReqs; *bytes = bytes used, *out_stride = output bytes per request.
+// On an error, *first_bad is the first request (in batch order) with a
+// shape error, and the requests before it are laid out.
+static int plan_batch(const ft_request* reqs, size_t batch, const StageLimits& lim,
+                      uint8_t* H, uint64_t cap, StagedReq* staged, uint64_t* bytes,
+                      uint64_t* out_stride, size_t* first_bad_out, std::string* msg) {
   DevReq* D = (DevReq*)H;
   uint64_t off = align_up(batch * sizeof(DevReq), 256);
   uint64_t max_out = sizeof(OutHeader);
@@ -996,19 +1034,21 @@ static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& l
       bad(FT_E_ARG, who() + "null topk_logp rows");
       break;
     }
-    // the block: lnf[T + 1] f64, beams[T], rows (token, logp, index), key
-    // bounds; it must fit before anything is written
+    // the block: lnf[T + 1] f64, beams[T], key bounds, rows (token, logp),
+    // then the row indices, which the kernel reads only when some row came
+    // out of order; it must fit before anything is written
     uint64_t o = align_up(8ull * (T + 1), 16);
     d.beams_off = (uint32_t)o;
     o = align_up(o + 4ull * T, 16);
+    d.kb_off = (uint32_t)o;
+    o = align_up(o + 16ull * T, 16);
     d.rid_off = (uint32_t)o;
     o = align_up(o + 4ull * T * K, 16);
     d.rlp_off = (uint32_t)o;
     o = align_up(o + 4ull * T * K, 16);
     d.rk_off = (uint32_t)o;
-    o = align_up(o + 2ull * T * K, 16);
-    d.kb_off = (uint32_t)o;
-    o = align_up(o + 16ull * T, 16);
+    d.in_bytes = (uint32_t)align_up(o + 2ull * T * K, 16);
+    o = d.in_bytes;
     if (off + o > cap) {
       bad(FT_E_LIMIT, who() + "the staged batch exceeds the staging buffer (" +
                           std::to_string(cap) + " bytes)");
@@ -1032,15 +1072,33 @@ static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& l
     st.out_bytes = step_stats_offset(F, T) + 8ull * kStepStats * T;
     max_out = std::max(max_out, st.out_bytes);
   }
+  *first_bad_out = first_bad;
+  *out_stride = align_up(max_out, 256);
+  *bytes = off;
+  if (first_bad != batch) return *msg = first_msg, first_rc;
+  return FT_OK;
+}
+
+// Validates `batch` requests and packs them into H (cap bytes), laid out by
+// plan_batch.  `tmp` holds max_topk pairs (the buffer an unsorted row is
+// sorted in).  An error names the first request (in batch order) that has
+// one.  Allocates nothing on success.
+static int pack_batch(const ft_request* reqs, size_t batch, const StageLimits& lim,
+                      uint8_t* H, uint64_t cap, StagedReq* staged,
+                      std::pair<uint32_t, uint32_t>* tmp, uint64_t* bytes,
+                      uint64_t* out_stride) {
+  size_t first_bad = batch;
+  std::string plan_msg;
+  const int plan_rc = plan_batch(reqs, batch, lim, H, cap, staged, bytes, out_stride,
+                                 &first_bad, &plan_msg);
   // the blocks of the requests before the first shape error
+  DevReq* D = (DevReq*)H;
   for (size_t r = 0; r < first_bad; ++r) {
     if (staged[r].skip) continue;
     std::string msg;
     if (int rc = pack_request(reqs[r], r, D[r], H + D[r].in_off, tmp, &msg)) return fail(rc, msg);
   }
-  if (first_bad != batch) return fail(first_rc, first_msg);
-  *out_stride = align_up(max_out, 256);
-  *bytes = off;
+  if (plan_rc) return fail(plan_rc, plan_msg);
   return FT_OK;
 }
 
@@ -1115,6 +1173,10 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.louds_words = c->d_louds_words;
   a.louds_z = c->d_louds_z;
   a.louds_s = c->d_louds_s;
+  a.stage_src = nullptr;
+  a.ready = nullptr;
+  a.out_host = nullptr;
+  a.stage_bytes = 0;
   return a;
 }
 
@@ -1242,9 +1304,9 @@ static int unpack_results(const uint8_t* h_out, uint64_t out_stride, const Stage
       if (!first_err) {
         first_err = o.status;
         g_err = "request " + std::to_string(r) +
-                ((oh->status & kStatusHistory)
-                     ? ": hypotheses exceed max_num_inter_beams"
-                     : ": kernel status " + std::to_string(oh->status));
+                ((oh->status & kStatusHistory)    ? ": hypotheses exceed max_num_inter_beams"
+                 : (oh->status & kStatusNotReady) ? ": its staged data was not ready in time"
+                                                  : ": kernel status " + std::to_string(oh->status));
       }
       continue;
     }
@@ -1298,13 +1360,85 @@ int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
                         batch, res, c->wall_khz, ms, timing);
 }
 
+// A streamed search: the kernel is launched as soon as the batch's shapes
+// are checked and laid out, and the requests are packed into mapped host
+// memory while it runs.  A request's leader starts once the request's
+// ready word is written, copies the packed block to the device itself and
+// writes the results back to mapped host memory, so packing overlaps the
+// launch and the search of the requests before it, and no copy engine sits
+// on the path.  Errors are those of ft_stage + ft_launch + ft_fetch: a
+// request that fails to pack is withdrawn (with every later one), the
+// kernel is waited for, and the first error in request order is returned.
 int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
               ft_result* results, ft_timing* timing) {
-  int rc = ft_stage(c, reqs, batch);
-  if (rc) return rc;
-  rc = ft_launch(c);
-  if (rc) return rc;
-  return ft_fetch(c, results, batch, timing);
+  if (!c || (!reqs && batch) || (!results && batch))
+    return fail(FT_E_ARG, "ft_search: null argument");
+  if (!c->reserved) return fail(FT_E_STATE, "ft_search: init_tbs_gpu (ft_reserve) was not called");
+  if (batch == 0 || batch > c->max_batch || batch > c->max_staged)
+    return fail(FT_E_LIMIT, "ft_search: batch size " + std::to_string(batch) + " not in [1, " +
+                                std::to_string(std::min(c->max_batch, c->max_staged)) + "]");
+  (void)hipSetDevice(c->device);
+  // a staging copy of ft_stage may still be queued: it reads h_stage
+  if (c->stage_pending) {
+    const hipError_t we = hipEventSynchronize(c->stage_ev);
+    if (we != hipSuccess) return hip_fail(we, "hipEventSynchronize(stage)");
+    c->stage_pending = false;
+  }
+  c->staged.assign(batch, StagedReq());
+  c->launched_slot.assign(batch, 0);
+  c->launched = false;
+  const StageLimits lim{c->max_steps, c->max_topk, c->max_out_beams, c->max_out_tokens};
+  DevReq* D = (DevReq*)c->h_stage;
+  auto drop = [c](int rc) {
+    c->staged.clear();
+    c->launched_slot.clear();
+    return rc;
+  };
+  uint64_t used = 0;
+  size_t first_bad = batch;
+  std::string msg;
+  if (int rc = plan_batch(reqs, batch, lim, c->h_stage, c->stage_cap, c->staged.data(), &used,
+                          &c->out_stride, &first_bad, &msg)) {
+    // a packing error of a request before the first shape error comes first
+    for (size_t r = 0; r < first_bad; ++r) {
+      if (c->staged[r].skip) continue;
+      std::string m;
+      if (int prc = pack_request(reqs[r], r, D[r], c->h_stage + D[r].in_off, c->sort_tmp.data(), &m))
+        return drop(fail(prc, m));
+    }
+    return drop(fail(rc, msg));
+  }
+  uint32_t kmax = 1;
+  for (size_t i = 0; i < batch; ++i) kmax = std::max(kmax, c->staged[i].K);
+  KArgs a = kernel_args(c, c->d_stage, 0, batch, kmax, c->d_ws, c->ws_stride, c->lay, c->d_out,
+                        c->out_stride);
+  a.reqs = (const DevReq*)c->m_stage;
+  a.stage_src = c->m_stage;
+  a.ready = c->m_ready;
+  a.out_host = c->m_out;
+  a.stage_bytes = used;
+  if (int rc = launch_timed(c, a)) return drop(rc);
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  int prc = FT_OK;
+  std::string pmsg;
+  for (size_t r = 0; r < batch; ++r) {
+    if (c->staged[r].skip) continue;  // its workgroups return at once
+    if (prc == FT_OK)
+      prc = pack_request(reqs[r], r, D[r], c->h_stage + D[r].in_off, c->sort_tmp.data(), &pmsg);
+    // the block's stores (non-temporal ones included) before the word
+    _mm_sfence();
+    __atomic_store_n(&c->h_ready[r], tag | (prc ? kReadyWithdrawn : kReadyOk), __ATOMIC_RELEASE);
+  }
+  double ms = 0.0;
+  if (int rc = ft_sync(c, &ms)) return drop(rc);
+  if (prc) return drop(fail(prc, pmsg));
+  for (size_t r = 0; r < batch; ++r) c->launched_slot[r] = 1;
+  const int rc = unpack_results(c->h_out, c->out_stride, c->staged.data(),
+                                c->launched_slot.data(), batch, results, c->wall_khz, ms, timing);
+  // the results were taken here: d_out holds no batch for ft_fetch
+  c->staged.clear();
+  c->launched_slot.clear();
+  return rc;
 }
 
 // Host side of the no-allocation path: pageable buffers in the library's

@@ -20,25 +20,37 @@ enum : uint32_t {
   kStatusOverflow = 1u,  // candidate buffer too small (never expected)
   kStatusHistory = 2u,   // history capacity (max_num_inter_beams) exceeded
   kStatusCorrupt = 4u,   // a link-parent walk did not terminate
+  kStatusWithdrawn = 8u, // streamed search: the host withdrew the request
+  kStatusNotReady = 16u, // streamed search: its ready word never came
+  kStatusStage = 32u,    // streamed search: the packed block is out of bounds
 };
 
+// Streamed search: the ready word of a request, (launch epoch << 32) | state,
+// written by the host once the request's block is packed (or withdrawn).
+enum : uint32_t { kReadyOk = 1u, kReadyWithdrawn = 2u };
+// How long a leader waits for its ready word (wall-clock ticks of 10 ns).
+constexpr unsigned long long kReadyTicks = 100000000ull;
+
 // Per-request descriptor, packed by the host at the start of the staging
-// buffer.  Offsets are relative to in_off.
+// buffer.  Offsets are relative to in_off; the block holds lnf[T + 1] (f64,
+// at offset 0), beams, key bounds, then the rows.
 struct DevReq {
   uint32_t T, K, F, flags;
   float tok_thr;
   uint32_t kb_off;     // u64[2T]: per step, bounds of its next-list keys
   double sent_thr;
   uint64_t in_off;     // byte offset of this request's block in the stage
-  uint32_t beams_off;  // lnf[T + 1] (f64) sits at offset 0
+  uint32_t beams_off;
   // proposal rows in ascending token order: token (u32[T * K]), logp
-  // (f32[T * K]) and the proposal's index in the caller's row (u16[T * K])
+  // (f32[T * K]) and the proposal's index in the caller's row (u16[T * K]);
+  // rk_off is 0 when every row came in ascending order (index = position)
   uint32_t rid_off;
   uint32_t rlp_off;
   uint32_t rk_off;
-  uint32_t pad0;
-  uint32_t out_T;        // token stride of the output rows
+  uint32_t in_bytes;   // bytes of the block the kernel reads (16-aligned)
+  uint32_t out_T;      // token stride of the output rows
 };
+static_assert(sizeof(DevReq) == 64, "DevReq layout");
 
 struct CurRec {     // a hypothesis kept in the beam
   double s;         // f64 sum of logps
@@ -222,6 +234,17 @@ struct KArgs {
   const uint64_t* louds_words;  // the LOUDS bits, 64 a word
   const uint32_t* louds_z;      // zeros before each 512-bit block
   const uint32_t* louds_s;      // block of every kLoudsSel-th zero
+  // Streamed search (null otherwise): `reqs` and the staged blocks sit in
+  // host memory mapped for the device (stage_src), where the host packs
+  // each request after the launch.  A request's leader waits for its ready
+  // word, copies its block to `stage` (stage_bytes long), and writes its
+  // results (header, norms, lengths, tokens) to out_host instead of `out`,
+  // where the per-step profile is kept during the search and copied to
+  // out_host at the end.
+  const uint8_t* stage_src;
+  const unsigned long long* ready;
+  uint8_t* out_host;
+  uint64_t stage_bytes;
 };
 
 // LOUDS directory of the trie's shape: for every node v in breadth-first

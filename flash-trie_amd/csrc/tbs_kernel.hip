@@ -654,24 +654,30 @@ __device__ __forceinline__ uint64_t louds_select0(const KArgs& a, uint32_t i) {
     if (a.louds_z[mid] <= i) lo = mid; else hi = mid - 1;
   }
   uint32_t r = i - a.louds_z[lo];
+  // the word holding it: walk the block's words, two per 16-byte read,
+  // while r is past their zeros (the block holds zero i, so the walk stops
+  // inside it); one read at a time keeps few registers live
   const uint4* line = (const uint4*)(a.louds_words + (uint64_t)lo * (kLoudsBlockBits / 64));
-  const uint4 q0 = line[0], q1 = line[1], q2 = line[2], q3 = line[3];
-  const uint64_t w[8] = {(uint64_t)q0.x | ((uint64_t)q0.y << 32), (uint64_t)q0.z | ((uint64_t)q0.w << 32),
-                         (uint64_t)q1.x | ((uint64_t)q1.y << 32), (uint64_t)q1.z | ((uint64_t)q1.w << 32),
-                         (uint64_t)q2.x | ((uint64_t)q2.y << 32), (uint64_t)q2.z | ((uint64_t)q2.w << 32),
-                         (uint64_t)q3.x | ((uint64_t)q3.y << 32), (uint64_t)q3.z | ((uint64_t)q3.w << 32)};
-  // the word holding it: walk the words while r is past their zeros (the
-  // block holds zero i, so the walk stops inside it)
   uint32_t wi = 0;
-  uint64_t z = ~w[0];
-#pragma unroll
-  for (int j = 0; j < 7; ++j) {
-    const uint32_t c = (uint32_t)__popcll(~w[j]);
-    if (wi == (uint32_t)j && r >= c) {
-      r -= c;
-      wi = j + 1;
-      z = ~w[j + 1];
+  uint64_t z = 0;
+  for (uint32_t h = 0; h < kLoudsBlockBits / 128; ++h) {
+    const uint4 q = line[h];
+    const uint64_t z0 = ~((uint64_t)q.x | ((uint64_t)q.y << 32));
+    const uint64_t z1 = ~((uint64_t)q.z | ((uint64_t)q.w << 32));
+    const uint32_t c0 = (uint32_t)__popcll(z0);
+    if (r < c0) {
+      z = z0;
+      wi = 2 * h;
+      break;
     }
+    r -= c0;
+    const uint32_t c1 = (uint32_t)__popcll(z1);
+    if (r < c1 || h + 1 == kLoudsBlockBits / 128) {
+      z = z1;
+      wi = 2 * h + 1;
+      break;
+    }
+    r -= c1;
   }
   // the r-th set bit of z, by halving
   uint32_t pos = 0;
@@ -1205,6 +1211,80 @@ __device__ __forceinline__ void hash_row(uint32_t K, Smem& sm) {
   __syncthreads();
 }
 
+// The proposal's index in the caller's row at position p (jk's low 16 bits)
+// of the token-sorted row t: from the staged indices, or p itself when every
+// row came in ascending token order (none staged).
+__device__ __forceinline__ uint32_t caller_index(const uint16_t* rk, uint32_t t, uint32_t K,
+                                                 uint32_t jk) {
+  const uint32_t p = jk & 0xFFFFu;
+  return rk ? (uint32_t)rk[(uint64_t)t * K + p] : p;
+}
+
+// Streamed search, the leader's start: thread 0 waits (bounded) for the
+// request's ready word in host memory -- a system-scope acquire, so that
+// what the host packed before it is what the reads below see -- and the
+// workgroup then copies the packed block from mapped host memory to the
+// device stage, with device-coherent stores: helpers read its rows from
+// there in shared steps, after the leader's first post (which follows the
+// wait for these stores).  Returns the request's rk_off as packed (the rest
+// of its header was final at the launch), or kStageFailed when the host
+// withdrew the request or the word never came, after releasing the helpers
+// and reporting the status in out_host.
+constexpr uint32_t kStageFailed = 0xFFFFFFFFu;
+__device__ __forceinline__ uint32_t stage_in(const KArgs& a, uint32_t req, uint8_t* ws,
+                                             Smem& sm) {
+  const uint32_t tid = threadIdx.x;
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  if (tid == 0) {
+    const unsigned long long t0 = wall_clock64();
+    unsigned long long v = 0;
+    for (;;) {
+      v = __hip_atomic_load(a.ready + req, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      if ((v >> 32) == a.epoch || wall_clock64() - t0 > kReadyTicks) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    sm.bcast = v;
+  }
+  __syncthreads();
+  const unsigned long long v = sm.bcast;
+  const DevReq d = a.reqs[req];
+  const bool fits = d.in_off + d.in_bytes <= a.stage_bytes && (d.in_bytes & 15u) == 0;
+  if (v != (tag | kReadyOk) || !fits) {
+    if (tid == 0) {
+      st_dev(&((Ctl*)(ws + a.lay.ctl))->go, tag | kGoExit);
+      OutHeader* oh = (OutHeader*)(a.out_host + (uint64_t)req * a.out_stride);
+      oh->count = 0;
+      oh->status = v == (tag | kReadyWithdrawn) ? kStatusWithdrawn
+                   : v == (tag | kReadyOk)      ? kStatusStage
+                                                : kStatusNotReady;
+    }
+    return kStageFailed;
+  }
+  const uint4* src = (const uint4*)(a.stage_src + d.in_off);
+  unsigned long long* dst = (unsigned long long*)(const_cast<uint8_t*>(a.stage) + d.in_off);
+  const uint32_t n16 = d.in_bytes / 16u;
+  constexpr uint32_t kU = 8;  // loads in flight per thread
+  for (uint32_t i0 = 0; i0 < n16; i0 += kBlock * kU) {
+    uint4 w[kU];
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u) {
+      const uint32_t i = i0 + u * kBlock + tid;
+      if (i < n16) w[u] = src[i];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kU; ++u) {
+      const uint32_t i = i0 + u * kBlock + tid;
+      if (i < n16) {
+        st_dev(dst + 2 * i, pack2(w[u].x, w[u].y));
+        st_dev(dst + 2 * i + 1, pack2(w[u].z, w[u].w));
+      }
+    }
+  }
+  wait_stores();
+  __syncthreads();
+  return d.rk_off;
+}
+
 // A helper workgroup: waits for shared steps of its request and expands its
 // slice of the work items, until the leader posts the exit generation.
 __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
@@ -1284,7 +1364,8 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.nS = nS;
     sv.next_cap = a.lay.next_cap;
     sv.sel_cap = a.lay.sel_cap;
-    sv.lnf_next = lnf[t + 1];
+    sv.lnf_next = __longlong_as_double(
+        (long long)ld_relaxed((const unsigned long long*)lnf + t + 1));
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
     sv.keep_lds_max = 0;
@@ -1299,8 +1380,8 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
       uint32_t tok = 0;
       float lp = 0.0f;
       if (i < d.K) {
-        tok = rid[ro + i];
-        lp = rlp[ro + i];
+        tok = ld_relaxed(rid + ro + i);
+        lp = __uint_as_float(ld_relaxed((const uint32_t*)rlp + ro + i));
       }
       if (lds_par && i <= n_par) {
         sm.woff[i] = ld_relaxed(&sv.woff[i]);
@@ -1579,6 +1660,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   const uint32_t tid = threadIdx.x;
   if (g >= a.wgs) return;
 
+  // (a streamed request's header is final at the launch but for rk_off,
+  // which stage_in reads once the block is packed)
   const DevReq d = a.reqs[req];
   uint8_t* ws = a.ws + (uint64_t)req * a.ws_stride;
   if (d.flags & kReqSkip) {
@@ -1595,14 +1678,23 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   }
 
   // ---- the leader ----------------------------------------------------------
+  uint32_t rk_off = d.rk_off;
+  if (a.ready) {
+    rk_off = stage_in(a, req, ws, sm);
+    if (rk_off == kStageFailed) return;
+    rk_off = uni(rk_off);
+  }
+  // results go to out_host when it is set; the per-step profile is kept in
+  // `out` during the search and copied there at the end
   uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
-  OutHeader* oh = (OutHeader*)ob;
+  uint8_t* rb = a.out_host ? a.out_host + (uint64_t)req * a.out_stride : ob;
+  OutHeader* oh = (OutHeader*)rb;
   const uint8_t* in = a.stage + uni(d.in_off);
   const double* lnf = (const double*)in;
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
   const float* rlp = (const float*)(in + d.rlp_off);
-  const uint16_t* rk = (const uint16_t*)(in + d.rk_off);
+  const uint16_t* rk = rk_off ? (const uint16_t*)(in + rk_off) : nullptr;
   const uint32_t T = d.T, K = d.K, F = d.F;
   const bool early = (d.flags & kReqEarlyExit) != 0;
 
@@ -2024,7 +2116,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       auto sel_arr = [&](uint32_t i) {
         const SelRec& r = selA[i];
         if (!r.isnew) return 0u;
-        return 1u + rank[r.jk >> 16] * K + rk[(uint64_t)t * K + (r.jk & 0xFFFFu)];
+        return 1u + rank[r.jk >> 16] * K + caller_index(rk, t, K, r.jk);
       };
       auto sel_node = [&](uint32_t i) { return selA[i].node; };
       Bound b{0, 0, 0, 0, 1};
@@ -2089,7 +2181,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     auto nk = [&](uint32_t i) { return nextc[i].key; };
     auto na = [&](uint32_t i) {
       const uint32_t jk = nextc[i].jk;
-      return rank[jk >> 16] * K + rk[(uint64_t)t * K + (jk & 0xFFFFu)];
+      return rank[jk >> 16] * K + caller_index(rk, t, K, jk);
     };
     auto nn = [&](uint32_t i) { return nextc[i].node; };
     const bool collect = M <= (uint32_t)kKeepCap;
@@ -2286,7 +2378,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   if (tid == 0) st_dev(&ctl->go, tag | kGoExit);
 
   // ---- output: selected in ascending (norm, node id) -----------------------
-  double* onorm = (double*)(ob + sizeof(OutHeader));
+  double* onorm = (double*)(rb + sizeof(OutHeader));
   uint32_t* olen = (uint32_t*)(onorm + F);
   uint32_t* otok = olen + F;
   const uint32_t status = sm.status;
@@ -2343,6 +2435,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
   }
   __syncthreads();
+  if (a.out_host) {
+    const uint64_t so = step_stats_offset(d.F, d.out_T);
+    const uint64_t* ss = (const uint64_t*)(ob + so);
+    uint64_t* hs = (uint64_t*)(rb + so);
+    for (uint32_t i = tid; i < d.out_T * kStepStats; i += kBlock) hs[i] = ss[i];
+  }
   if (tid == 0) {
     oh->count = status ? 0 : nS;
     oh->status = status;

@@ -21,7 +21,8 @@
  *                  launch for the whole batch instead of one per request
  *   ft_fetch    -- copy_output_to_cpu (tbs-kernels.cu:742-835)
  *   ft_search   -- LoudsTrie::tbs_gpu / tbs_gpu_batched
- *                  (tbs-kernels.cu:673-700): stage + launch + fetch
+ *                  (tbs-kernels.cu:673-700): stage + launch + fetch,
+ *                  with the packing overlapping the search
  *   ft_destroy  -- ~BeamSearchState (tbs-kernels.cu:148-166)
  *
  * Search semantics are those of the reference CPU path LoudsTrie::tbs
@@ -193,7 +194,16 @@ int ft_launch_times(ft_ctx* ctx, double* ms, size_t n);
 int ft_fetch(ft_ctx* ctx, ft_result* results, size_t batch,
              ft_timing* timing);
 
-/* stage + launch + fetch. */
+/* The results of stage + launch + fetch, streamed: the kernel is launched
+ * once the batch's shapes are checked (errors of ft_stage's shape checks
+ * come before any launch), then each request is packed into pinned host
+ * memory mapped for the device while the kernel runs; a request's leader
+ * starts when its request is packed, copies it to the device and writes its
+ * results back to mapped host memory (no copy-engine transfers).  A request
+ * that fails to pack is withdrawn with every later one, the kernel is
+ * waited for, and the first error in request order is returned.  Afterwards
+ * ft_fetch has nothing to fetch (FT_E_STATE).  timing->kernel_ms spans the
+ * launch, which overlaps the packing. */
 int ft_search(ft_ctx* ctx, const ft_request* reqs, size_t batch,
               ft_result* results, ft_timing* timing);
 

@@ -58,7 +58,7 @@ int main() {
           ids[r][t * K + k] = v;
           lps[r][t * K + k] = -(float)(g() % 60) * 0.25f;
         }
-        if (g() % 3 == 0)  // shuffle: an unsorted row
+        if (g() % 3 == 0 && r % 2 == 0)  // shuffle: an unsorted row (even requests only)
           std::shuffle(ids[r].begin() + t * K, ids[r].begin() + (t + 1) * K, g);
         if (K > 1 && g() % 40 == 0) {
           ids[r][t * K + 1] = ids[r][t * K];
@@ -107,6 +107,21 @@ int main() {
       const float* rlp = (const float*)(base + d.rlp_off);
       const uint16_t* rk = (const uint16_t*)(base + d.rk_off);
       const uint64_t* kb = (const uint64_t*)(base + d.kb_off);
+      // the indices are staged iff some row is out of order; the kernel
+      // reads [0, in_bytes) of the block, which must hold every array
+      bool all_sorted = true;
+      for (uint32_t t = 0; t < T; ++t)
+        for (uint32_t k = 1; k < K; ++k)
+          if (ids[r][t * K + k] <= ids[r][t * K + k - 1]) all_sorted = false;
+      CHECK((d.rk_off == 0) == all_sorted, "case %d: rk_off %u, rows sorted %d", c, d.rk_off,
+            (int)all_sorted);
+      const uint64_t need = std::max<uint64_t>(
+          {8ull * (T + 1), d.beams_off + 4ull * T, d.kb_off + 16ull * T, d.rid_off + 4ull * T * K,
+           d.rlp_off + 4ull * T * K, d.rk_off ? d.rk_off + 2ull * T * K : 0ull});
+      CHECK(d.in_bytes >= need && d.in_bytes % 16 == 0 && d.in_bytes < need + 16,
+            "case %d: in_bytes %u for %lu", c, d.in_bytes, (unsigned long)need);
+      if (r + 1 < n)
+        CHECK(d.in_off + d.in_bytes <= D[r + 1].in_off, "case %d: blocks overlap", c);
       double s_lo = 0.0, s_hi = 0.0;
       for (uint32_t t = 0; t < T; ++t) {
         std::vector<std::pair<uint32_t, uint32_t>> e(K);
@@ -115,7 +130,8 @@ int main() {
         double x_lo = 0.0, x_hi = 0.0;
         bool any = false;
         for (uint32_t p = 0; p < K; ++p) {
-          CHECK(rid[t * K + p] == e[p].first && rk[t * K + p] == e[p].second &&
+          CHECK(rid[t * K + p] == e[p].first &&
+                    (d.rk_off ? (uint32_t)rk[t * K + p] : p) == e[p].second &&
                     rlp[t * K + p] == lps[r][t * K + e[p].second],
                 "case %d row %u pos %u", c, t, p);
           const double x = (double)lps[r][t * K + p];

@@ -199,6 +199,53 @@ def test_request_errors(ft, c1):
     assert_same_results((got[0][0], got[1][0]), want)
 
 
+@pytest.mark.parametrize("early", [False, True])
+def test_streamed_batches(ft, c1, early):
+    # bs_tbs_gpu packs each request after the launch and the kernel picks it
+    # up from host memory: batches of 8 mixing token-sorted rows with
+    # shuffled ones (whose caller indices are staged), a final beam of 0, and
+    # a request that fails to pack (withdrawn with the ones after it: the
+    # call fails naming it, and the next call on the context works)
+    t, o, ids, lp = c1
+    rng = np.random.default_rng(11)
+    for b0 in range(0, 64, 8):
+        beams, bi, bl = [], [], []
+        for i in range(8):
+            r = b0 + i
+            i2, l2 = ids[r], lp[r]
+            if rng.integers(2):
+                perm = np.stack([rng.permutation(32) for _ in range(8)])
+                i2 = np.take_along_axis(i2, perm, 1)
+                l2 = np.take_along_axis(l2, perm, 1)
+            bw = [int(x) for x in rng.integers(1, 11, 8)]
+            if i == 3 and b0 == 8:
+                bw[-1] = 0
+            beams.append(bw)
+            bi.append(i2)
+            bl.append(l2)
+        print("streamed batch", b0, "early", early, flush=True)
+        s, n, _, _ = ft.bs_tbs_gpu(t, 8, beams, [x.tolist() for x in bi],
+                                   [x.tolist() for x in bl], -10.0, -40.0, 5.0, early)
+        for i in range(8):
+            if beams[i][-1] == 0:
+                assert s[i] == [] and list(n[i]) == []
+                continue
+            want = o.tbs(beams[i], bi[i], bl[i], -10.0, -40.0, 5.0, early)
+            assert_same_results((s[i], n[i]), want, f"streamed {b0}+{i}")
+    rows = [ids[r].tolist() for r in range(8)]
+    lps = [lp[r].tolist() for r in range(8)]
+    lps[5] = lp[5].copy()
+    lps[5][2, 7] = np.nan
+    lps[5] = lps[5].tolist()
+    with pytest.raises(RuntimeError, match="request 5: topk_logp holds NaN"):
+        ft.bs_tbs_gpu(t, 8, [[10] * 8] * 8, rows, lps, -10.0, -40.0, 5.0, early)
+    s, n, _, _ = ft.bs_tbs_gpu(t, 8, [[10] * 8] * 8, rows,
+                               [lp[r].tolist() for r in range(8)], -10.0, -40.0, 5.0, early)
+    for i in range(8):
+        want = o.tbs([10] * 8, ids[i], lp[i], -10.0, -40.0, 5.0, early)
+        assert_same_results((s[i], n[i]), want, f"after the withdrawn batch, {i}")
+
+
 def test_history_limit_is_an_error(ft):
     toks, offs = ft.synth_keys(5000, 256, 3, 6, 1.1, 1)
     t = ft.Trie()
