@@ -1377,6 +1377,13 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
   if (batch == 0 || batch > c->max_batch || batch > c->max_staged)
     return fail(FT_E_LIMIT, "ft_search: batch size " + std::to_string(batch) + " not in [1, " +
                                 std::to_string(std::min(c->max_batch, c->max_staged)) + "]");
+  if (c->d_louds_words) {
+    // the LOUDS directory's kernel has no streamed form
+    int rc = ft_stage(c, reqs, batch);
+    if (!rc) rc = ft_launch(c);
+    if (!rc) rc = ft_fetch(c, results, batch, timing);
+    return rc;
+  }
   (void)hipSetDevice(c->device);
   // a staging copy of ft_stage may still be queued: it reads h_stage
   if (c->stage_pending) {

@@ -91,6 +91,9 @@ struct alignas(16) Smem {
   unsigned long long tiny_cands, tiny_ticks;
   uint32_t par_w;       // work items of a step with at most 64 parents
   uint32_t w_children, w_probes;
+  // where the leader writes its results: out_host's block of the request,
+  // or null for `out` (kept here rather than in registers through the steps)
+  unsigned long long res_host;
   // expansion: the current proposal row in ascending token order
   alignas(16) uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
@@ -1287,6 +1290,7 @@ __device__ __forceinline__ uint32_t stage_in(const KArgs& a, uint32_t req, uint8
 
 // A helper workgroup: waits for shared steps of its request and expands its
 // slice of the work items, until the leader posts the exit generation.
+template <bool kStreamed>
 __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uint8_t* ws,
                             uint32_t g, Smem& sm) {
   const uint32_t tid = threadIdx.x;
@@ -1364,8 +1368,13 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.nS = nS;
     sv.next_cap = a.lay.next_cap;
     sv.sel_cap = a.lay.sel_cap;
-    sv.lnf_next = __longlong_as_double(
-        (long long)ld_relaxed((const unsigned long long*)lnf + t + 1));
+    // (a streamed search's leader wrote the stage during this launch: read
+    // it device-coherently; a staged one's was copied before the launch)
+    if constexpr (kStreamed)
+      sv.lnf_next = __longlong_as_double(
+          (long long)ld_relaxed((const unsigned long long*)lnf + t + 1));
+    else
+      sv.lnf_next = lnf[t + 1];
     sv.tok_thr = d.tok_thr;
     sv.sent_thr = d.sent_thr;
     sv.keep_lds_max = 0;
@@ -1380,8 +1389,13 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
       uint32_t tok = 0;
       float lp = 0.0f;
       if (i < d.K) {
-        tok = ld_relaxed(rid + ro + i);
-        lp = __uint_as_float(ld_relaxed((const uint32_t*)rlp + ro + i));
+        if constexpr (kStreamed) {
+          tok = ld_relaxed(rid + ro + i);
+          lp = __uint_as_float(ld_relaxed((const uint32_t*)rlp + ro + i));
+        } else {
+          tok = rid[ro + i];
+          lp = rlp[ro + i];
+        }
       }
       if (lds_par && i <= n_par) {
         sm.woff[i] = ld_relaxed(&sv.woff[i]);
@@ -1647,9 +1661,11 @@ __device__ __forceinline__ void tiny_steps(
 }
 
 // kLouds: child ranges from the LOUDS directory (KArgs::louds_*) instead
-// of the node records -- a separate instantiation, so that the records'
-// kernel keeps its own register allocation.
-template <bool kLouds>
+// of the node records; kStreamed: the streamed search (KArgs::ready and
+// friends).  Separate instantiations, so that each keeps its own register
+// allocation and code: the staged search carries none of the streamed
+// one's start and output.
+template <bool kLouds, bool kStreamed>
 __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   __shared__ Smem sm;
   // request-major interleave: request r owns blocks r, r + batch, ...  The
@@ -1673,22 +1689,21 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     return;
   }
   if (g != 0) {
-    helper_loop(a, d, ws, g, sm);
+    helper_loop<kStreamed>(a, d, ws, g, sm);
     return;
   }
 
   // ---- the leader ----------------------------------------------------------
   uint32_t rk_off = d.rk_off;
-  if (a.ready) {
+  // the per-step profile goes to `out` during the search; the results (and
+  // a copy of the profile) to out_host in a streamed search, else to `out`
+  uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
+  if constexpr (kStreamed) {
     rk_off = stage_in(a, req, ws, sm);
     if (rk_off == kStageFailed) return;
     rk_off = uni(rk_off);
+    if (tid == 0) sm.res_host = (unsigned long long)(a.out_host + (uint64_t)req * a.out_stride);
   }
-  // results go to out_host when it is set; the per-step profile is kept in
-  // `out` during the search and copied there at the end
-  uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
-  uint8_t* rb = a.out_host ? a.out_host + (uint64_t)req * a.out_stride : ob;
-  OutHeader* oh = (OutHeader*)rb;
   const uint8_t* in = a.stage + uni(d.in_off);
   const double* lnf = (const double*)in;
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
@@ -2378,6 +2393,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   if (tid == 0) st_dev(&ctl->go, tag | kGoExit);
 
   // ---- output: selected in ascending (norm, node id) -----------------------
+  // (out_host's block is formed as an offset from `ob`, so that the
+  // compiler keeps global -- not flat -- stores for it: a mapped host
+  // address is a global one too)
+  uint8_t* rb = ob;
+  if constexpr (kStreamed) rb = ob + (int64_t)(uni((uint64_t)sm.res_host) - (uint64_t)ob);
+  OutHeader* oh = (OutHeader*)rb;
   double* onorm = (double*)(rb + sizeof(OutHeader));
   uint32_t* olen = (uint32_t*)(onorm + F);
   uint32_t* otok = olen + F;
@@ -2435,7 +2456,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
   }
   __syncthreads();
-  if (a.out_host) {
+  if constexpr (kStreamed) {
     const uint64_t so = step_stats_offset(d.F, d.out_T);
     const uint64_t* ss = (const uint64_t*)(ob + so);
     uint64_t* hs = (uint64_t*)(rb + so);
@@ -2511,12 +2532,15 @@ hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64
 // and the leader takes over the slices no helper has claimed), so the grid
 // needs no co-residency guarantee.
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
-  if (args.louds_words)
-    hipLaunchKernelGGL(tbs_kernel<true>, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream,
-                       args);
-  else
-    hipLaunchKernelGGL(tbs_kernel<false>, dim3(args.batch * args.wgs), dim3(kBlock), 0, stream,
-                       args);
+  const dim3 grid(args.batch * args.wgs), block(kBlock);
+  if (args.louds_words) {
+    if (args.ready) return hipErrorInvalidValue;  // (no streamed LOUDS search)
+    hipLaunchKernelGGL((tbs_kernel<true, false>), grid, block, 0, stream, args);
+  } else if (args.ready) {
+    hipLaunchKernelGGL((tbs_kernel<false, true>), grid, block, 0, stream, args);
+  } else {
+    hipLaunchKernelGGL((tbs_kernel<false, false>), grid, block, 0, stream, args);
+  }
   return hipGetLastError();
 }
 
@@ -2524,7 +2548,7 @@ int tbs_block_threads() { return kBlock; }
 
 int tbs_max_resident_blocks(int num_cus) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)tbs_kernel<false>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)tbs_kernel<false, false>,
                                                    kBlock, 0) != hipSuccess)
     return 0;
   return per_cu * num_cus;
