@@ -8,7 +8,7 @@
 // tbs-kernels.cu:686-700).
 #include <hip/hip_runtime.h>
 
-#include <emmintrin.h>
+#include <immintrin.h>
 
 #include <algorithm>
 #include <atomic>
@@ -817,8 +817,8 @@ struct RowScan {
   bool bad, sorted;
   float lo, hi;
 };
-static RowScan scan_row(const uint32_t* rid, const float* rlp, uint32_t K, float thr,
-                        uint32_t* oid, float* olp) {
+static RowScan scan_row_sse2(const uint32_t* rid, const float* rlp, uint32_t K, float thr,
+                             uint32_t* oid, float* olp) {
   const __m128 vinf = _mm_set1_ps(INFINITY), vninf = _mm_set1_ps(-INFINITY);
   const __m128 vthr = _mm_set1_ps(thr);
   const __m128i flip = _mm_set1_epi32((int)0x80000000u), ones = _mm_set1_epi32(-1);
@@ -871,6 +871,68 @@ static RowScan scan_row(const uint32_t* rid, const float* rlp, uint32_t K, float
   return RowScan{bad, sorted, lo, hi};
 }
 
+// The same scan, eight proposals at a time (AVX2 hosts).
+__attribute__((target("avx2"))) static RowScan scan_row_avx2(const uint32_t* rid,
+                                                             const float* rlp, uint32_t K,
+                                                             float thr, uint32_t* oid,
+                                                             float* olp) {
+  const __m256 vinf = _mm256_set1_ps(INFINITY), vninf = _mm256_set1_ps(-INFINITY);
+  const __m256 vthr = _mm256_set1_ps(thr);
+  const __m256i flip = _mm256_set1_epi32((int)0x80000000u), ones = _mm256_set1_epi32(-1);
+  bool bad = false, sorted = true;
+  float lo = INFINITY, hi = -INFINITY;
+  uint32_t k = 1;
+  if (K >= 9) {
+    __m256 vlo = vinf, vhi = vninf, vbad = _mm256_setzero_ps();
+    __m256i vuns = _mm256_setzero_si256();
+    for (; k + 8 <= K; k += 8) {
+      const __m256 x = _mm256_loadu_ps(rlp + k);
+      _mm256_storeu_ps(olp + k, x);
+      vbad = _mm256_or_ps(vbad, _mm256_or_ps(_mm256_cmp_ps(x, x, _CMP_UNORD_Q),
+                                             _mm256_cmp_ps(x, vinf, _CMP_EQ_OQ)));
+      const __m256 keep = _mm256_cmp_ps(x, vthr, _CMP_GT_OQ);
+      vlo = _mm256_min_ps(vlo, _mm256_blendv_ps(vinf, x, keep));
+      vhi = _mm256_max_ps(vhi, _mm256_blendv_ps(vninf, x, keep));
+      // unsigned rid[i] > rid[i - 1] as a signed compare of flipped words
+      const __m256i ra = _mm256_loadu_si256((const __m256i*)(rid + k));
+      _mm256_storeu_si256((__m256i*)(oid + k), ra);
+      const __m256i a = _mm256_xor_si256(ra, flip);
+      const __m256i b = _mm256_xor_si256(_mm256_loadu_si256((const __m256i*)(rid + k - 1)), flip);
+      vuns = _mm256_or_si256(vuns, _mm256_xor_si256(_mm256_cmpgt_epi32(a, b), ones));
+    }
+    alignas(32) float l8[8], h8[8];
+    alignas(32) uint32_t b8[8], u8[8];
+    _mm256_store_ps(l8, vlo);
+    _mm256_store_ps(h8, vhi);
+    _mm256_store_si256((__m256i*)b8, _mm256_castps_si256(vbad));
+    _mm256_store_si256((__m256i*)u8, vuns);
+    for (int j = 0; j < 8; ++j) {
+      lo = std::min(lo, l8[j]);
+      hi = std::max(hi, h8[j]);
+      bad = bad || b8[j] != 0;
+      sorted = sorted && u8[j] == 0;
+    }
+  }
+  auto one = [&](uint32_t i) {
+    const float x = rlp[i];
+    olp[i] = x;
+    oid[i] = rid[i];
+    bad = bad || std::isnan(x) || x == INFINITY;
+    if (x > thr) {
+      lo = std::min(lo, x);
+      hi = std::max(hi, x);
+    }
+    if (i > 0 && rid[i] <= rid[i - 1]) sorted = false;
+  };
+  if (K) one(0);
+  for (; k < K; ++k) one(k);
+  return RowScan{bad, sorted, lo, hi};
+}
+
+using ScanRowFn = RowScan (*)(const uint32_t*, const float*, uint32_t, float, uint32_t*, float*);
+static const ScanRowFn g_scan_row =
+    __builtin_cpu_supports("avx2") ? scan_row_avx2 : scan_row_sse2;
+
 // Packs one validated request into its block at `base` (see plan_batch):
 // the length-norm table, beam widths, per-step key bounds and token-sorted
 // rows, and sets d.rk_off / d.in_bytes: the proposals' indices in the
@@ -915,7 +977,7 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
     uint32_t* oid = rid_s + (uint64_t)t * K;
     float* olp = rlp_s + (uint64_t)t * K;
     uint16_t* ok = rk_s + (uint64_t)t * K;
-    const RowScan sc = scan_row(rid, rlp, K, q.token_logp_threshold, oid, olp);
+    const RowScan sc = g_scan_row(rid, rlp, K, q.token_logp_threshold, oid, olp);
     if (sc.bad) return *err = who() + "topk_logp holds NaN or +inf", FT_E_INPUT;
     if (sc.sorted) {
       if (rk_used)
@@ -1360,6 +1422,34 @@ int ft_fetch(ft_ctx* c, ft_result* res, size_t batch, ft_timing* timing) {
                         batch, res, c->wall_khz, ms, timing);
 }
 
+namespace {
+struct PackJob {
+  const ft_request* reqs;
+  DevReq* D;
+  uint8_t* H;
+  const StagedReq* staged;
+  unsigned long long* ready;
+  unsigned long long tag;
+  size_t batch;
+  std::vector<int> rc;
+  std::vector<std::string> msg;
+};
+
+// Packs the requests of `j` in order, writing each one's ready word as soon
+// as it is packed (a skipped request's workgroups return at once and need
+// none); `tmp` holds max_topk pairs.
+void pack_stream(PackJob& j, std::pair<uint32_t, uint32_t>* tmp) {
+  for (size_t r = 0; r < j.batch; ++r) {
+    if (j.staged[r].skip) continue;
+    const int rc = pack_request(j.reqs[r], r, j.D[r], j.H + j.D[r].in_off, tmp, &j.msg[r]);
+    j.rc[r] = rc;
+    // the block's stores (non-temporal ones included) before the word
+    _mm_sfence();
+    __atomic_store_n(&j.ready[r], j.tag | (rc ? kReadyWithdrawn : kReadyOk), __ATOMIC_RELEASE);
+  }
+}
+}  // namespace
+
 // A streamed search: the kernel is launched as soon as the batch's shapes
 // are checked and laid out, and the requests are packed into mapped host
 // memory while it runs.  A request's leader starts once the request's
@@ -1425,20 +1515,21 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
   a.out_host = c->m_out;
   a.stage_bytes = used;
   if (int rc = launch_timed(c, a)) return drop(rc);
-  const unsigned long long tag = (unsigned long long)a.epoch << 32;
-  int prc = FT_OK;
-  std::string pmsg;
-  for (size_t r = 0; r < batch; ++r) {
-    if (c->staged[r].skip) continue;  // its workgroups return at once
-    if (prc == FT_OK)
-      prc = pack_request(reqs[r], r, D[r], c->h_stage + D[r].in_off, c->sort_tmp.data(), &pmsg);
-    // the block's stores (non-temporal ones included) before the word
-    _mm_sfence();
-    __atomic_store_n(&c->h_ready[r], tag | (prc ? kReadyWithdrawn : kReadyOk), __ATOMIC_RELEASE);
-  }
+  PackJob job;
+  job.reqs = reqs;
+  job.D = D;
+  job.H = c->h_stage;
+  job.staged = c->staged.data();
+  job.ready = c->h_ready;
+  job.tag = (unsigned long long)a.epoch << 32;
+  job.batch = batch;
+  job.rc.assign(batch, FT_OK);
+  job.msg.resize(batch);
+  pack_stream(job, c->sort_tmp.data());
   double ms = 0.0;
   if (int rc = ft_sync(c, &ms)) return drop(rc);
-  if (prc) return drop(fail(prc, pmsg));
+  for (size_t r = 0; r < batch; ++r)  // the first packing error in request order
+    if (job.rc[r]) return drop(fail(job.rc[r], job.msg[r]));
   for (size_t r = 0; r < batch; ++r) c->launched_slot[r] = 1;
   const int rc = unpack_results(c->h_out, c->out_stride, c->staged.data(),
                                 c->launched_slot.data(), batch, results, c->wall_khz, ms, timing);

@@ -347,8 +347,10 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
   std::vector<std::vector<const uint32_t*>> idrows(B);
   std::vector<std::vector<const float*>> lprows(B);
   std::vector<Shape> shapes(B);
-  std::vector<std::vector<double>> norms(B);
-  std::vector<std::vector<uint32_t>> lens(B), toks(B);
+  // result arrays, left uninitialised: the search writes the first count
+  // entries of each, and only those are read
+  std::vector<std::unique_ptr<double[]>> norms(B);
+  std::vector<std::unique_ptr<uint32_t[]>> lens(B), toks(B);
   for (size_t b = 0; b < B; ++b) {
     const TbsInput& in = inputs[b];
     shapes[b] = check_shape(in);
@@ -374,14 +376,14 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
     q.topk_id_rows = idrows[b].data();
     q.topk_logp_rows = lprows[b].data();
     const size_t F = shapes[b].F;
-    norms[b].resize(F);
-    lens[b].resize(F);
-    toks[b].resize(F * T);
+    norms[b].reset(new double[F]);
+    lens[b].reset(new uint32_t[F]);
+    toks[b].reset(new uint32_t[F * T]);
     res[b].capacity = (uint32_t)F;
     res[b].token_stride = (uint32_t)T;
-    res[b].logp_norm = norms[b].data();
-    res[b].length = lens[b].data();
-    res[b].tokens = toks[b].data();
+    res[b].logp_norm = norms[b].get();
+    res[b].length = lens[b].get();
+    res[b].tokens = toks[b].get();
   }
   int rc;
   {
@@ -395,9 +397,9 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
     const ft_result& o = res[b];
     const size_t T = shapes[b].T;
     in.out_sent.resize(o.count);
-    in.out_logp_norm.assign(norms[b].begin(), norms[b].begin() + o.count);
+    in.out_logp_norm.assign(norms[b].get(), norms[b].get() + o.count);
     for (uint32_t i = 0; i < o.count; ++i)
-      in.out_sent[i].assign(toks[b].begin() + i * T, toks[b].begin() + i * T + lens[b][i]);
+      in.out_sent[i].assign(toks[b].get() + i * T, toks[b].get() + i * T + lens[b][i]);
     in.t_expansion_ms = o.device_ms[0];
     in.t_validation_ms = 0.0;
     in.t_selection_ms = o.device_ms[1];

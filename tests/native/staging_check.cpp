@@ -8,6 +8,7 @@
 #include "ft_runtime.cpp"
 
 #include <cstdio>
+#include <memory>
 #include <random>
 
 namespace ftk {  // the device side is not linked here
@@ -149,6 +150,87 @@ int main() {
       }
     }
   }
-  std::printf("%d batches packed, %d rejected, %d failures\n", cases, rejected, fails);
+  // The streamed search's packing: plan_batch lays the batch out, then
+  // pack_stream packs the requests and writes their ready words.  The blocks
+  // must equal pack_batch's; a request with a NaN is withdrawn (and only it
+  // -- the others stay ready), where pack_batch fails.
+  int streamed = 0;
+  std::vector<uint8_t> H2(8 << 20);
+  std::vector<StagedReq> st2(8);
+  std::vector<unsigned long long> ready(8);
+  for (int c = 0; c < 400; ++c) {
+    const uint32_t T = 1 + g() % 6, K = 1 + g() % 300, n = 2 + g() % 7;
+    std::vector<std::vector<uint32_t>> beams(n), ids(n);
+    std::vector<std::vector<float>> lps(n);
+    std::vector<ft_request> reqs(n);
+    const uint32_t nan_req = (g() % 4 == 0) ? (uint32_t)(g() % n) : n;
+    for (uint32_t r = 0; r < n; ++r) {
+      beams[r].assign(T, 1 + (uint32_t)(g() % 9));
+      ids[r].resize((size_t)T * K);
+      lps[r].resize((size_t)T * K);
+      for (uint32_t t = 0; t < T; ++t) {
+        uint32_t v = (uint32_t)(g() % 5);
+        for (uint32_t k = 0; k < K; ++k) {
+          v += 1 + (uint32_t)(g() % 4);
+          ids[r][t * K + k] = v;
+          lps[r][t * K + k] = -(float)(g() % 60) * 0.25f;
+        }
+        if (g() % 3 == 0)
+          std::shuffle(ids[r].begin() + t * K, ids[r].begin() + (t + 1) * K, g);
+      }
+      if (r == nan_req) lps[r][g() % ((size_t)T * K)] = NAN;
+      ft_request& q = reqs[r];
+      std::memset(&q, 0, sizeof q);
+      q.beams = beams[r].data();
+      q.num_beams = T;
+      q.num_steps = T;
+      q.topk = K;
+      q.topk_id = ids[r].data();
+      q.topk_logp = lps[r].data();
+      q.token_logp_threshold = -5.0f;
+      q.sent_logp_threshold = -20.0;
+      q.length_norm = 2.0;
+    }
+    StageLimits lim{64, 4096, 1000, 1u << 20};
+    uint64_t used = 0, used2 = 0, os = 0, os2 = 0;
+    // (padding and unstaged row indices are left unwritten: start both alike)
+    std::memset(H.data(), 0, 1 << 20);
+    std::memset(H2.data(), 0, 1 << 20);
+    for (auto& x : st) x = StagedReq();
+    for (auto& x : st2) x = StagedReq();
+    const int rc1 = pack_batch(reqs.data(), n, lim, H.data(), H.size(), st.data(), tmp.data(),
+                               &used, &os);
+    size_t first_bad = n;
+    std::string msg;
+    const int rc2 = plan_batch(reqs.data(), n, lim, H2.data(), H2.size(), st2.data(), &used2,
+                               &os2, &first_bad, &msg);
+    CHECK(rc2 == FT_OK && used2 == used, "stream case %d: plan rc %d", c, rc2);
+    PackJob job;
+    job.reqs = reqs.data();
+    job.D = (DevReq*)H2.data();
+    job.H = H2.data();
+    job.staged = st2.data();
+    job.ready = ready.data();
+    job.tag = (unsigned long long)(c + 1) << 32;
+    job.batch = n;
+    job.rc.assign(n, FT_OK);
+    job.msg.resize(n);
+    pack_stream(job, tmp.data());
+    for (uint32_t r = 0; r < n; ++r) {
+      const bool bad = r == nan_req;
+      CHECK((job.rc[r] != FT_OK) == bad, "stream case %d request %u: rc %d", c, r, job.rc[r]);
+      CHECK(ready[r] == (job.tag | (bad ? kReadyWithdrawn : kReadyOk)),
+            "stream case %d request %u: ready word", c, r);
+    }
+    if (nan_req == n) {
+      CHECK(rc1 == FT_OK, "stream case %d: pack_batch rc %d", c, rc1);
+      CHECK(std::memcmp(H.data(), H2.data(), used) == 0, "stream case %d: blocks differ", c);
+      ++streamed;
+    } else {
+      CHECK(rc1 == FT_E_INPUT, "stream case %d: pack_batch rc %d", c, rc1);
+    }
+  }
+  std::printf("%d batches packed, %d rejected, %d streamed batches compared, %d failures\n",
+              cases, rejected, streamed, fails);
   return fails ? 1 : 0;
 }

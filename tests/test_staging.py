@@ -20,4 +20,4 @@ def test_packing_matches_scalar_restatement(tmp_path):
         stderr=subprocess.DEVNULL)
     p = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert p.returncode == 0, p.stdout
-    assert "0 failures" in p.stdout
+    assert "0 failures" in p.stdout and "0 streamed" not in p.stdout, p.stdout
