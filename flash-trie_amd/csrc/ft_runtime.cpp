@@ -102,6 +102,10 @@ struct ft_ctx {
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
 
   std::vector<StagedReq> staged;
+  // per request of a streamed search: taken, its error and error text
+  std::vector<uint8_t> req_got;
+  std::vector<int> req_rc;
+  std::vector<std::string> req_msg;
   std::vector<std::pair<uint32_t, uint32_t>> sort_tmp;  // max_topk pairs
   // staged requests launched since the last ft_stage (ft_fetch reports the
   // others as FT_E_STATE instead of returning whatever d_out holds)
@@ -1324,6 +1328,65 @@ int ft_sync(ft_ctx* c, double* ms) {
   return FT_OK;
 }
 
+// Fills `o` from request r's output block `ob` (in h_out, or in host
+// memory the kernel wrote directly) and adds its device counters to `tm`.
+// Returns the request's error (FT_OK when its results are in `o`), with
+// its text in *msg.
+static int unpack_one(const uint8_t* ob, const StagedReq& st, bool launched, size_t r,
+                      ft_result& o, double tick_ms, ft_timing& tm, std::string* msg) {
+  auto err = [&](int rc, const std::string& m) {
+    o.count = 0;
+    o.status = rc;
+    *msg = "request " + std::to_string(r) + m;
+    return rc;
+  };
+  if (!launched)  // staged but not launched since: no result of this request
+    return err(FT_E_STATE, ": staged but not launched");
+  if (st.skip) {
+    o.count = 0;
+    o.status = FT_OK;
+    return FT_OK;
+  }
+  const OutHeader* oh = (const OutHeader*)ob;
+  const uint32_t status = oh->status & ~kStatusDone;
+  tm.expand_ms += oh->ticks_expand * tick_ms;
+  tm.select_ms += oh->ticks_select * tick_ms;
+  tm.other_ms += (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
+  tm.candidates += oh->candidates;
+  tm.parents += oh->parents;
+  tm.children += oh->children;
+  tm.probes += oh->probes;
+  if (status)
+    return err((status & kStatusHistory) ? FT_E_LIMIT : FT_E_KERNEL,
+               (status & kStatusHistory)    ? ": hypotheses exceed max_num_inter_beams"
+               : (status & kStatusNotReady) ? ": its staged data was not ready in time"
+                                            : ": kernel status " + std::to_string(status));
+  const uint32_t n = oh->count;
+  if (n > o.capacity || (n && (!o.logp_norm || !o.length || !o.tokens)) ||
+      o.token_stride < st.T)
+    return err(FT_E_ARG, ": result arrays too small");
+  o.device_ms[0] = oh->ticks_expand * tick_ms;
+  o.device_ms[1] = oh->ticks_select * tick_ms;
+  o.device_ms[2] = (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
+  o.device_ms[3] = oh->ticks_total * tick_ms;
+  const double* norms = (const double*)(ob + sizeof(OutHeader));
+  const uint32_t* lens = (const uint32_t*)(norms + st.F);
+  const uint32_t* toks = lens + st.F;
+  std::memcpy(o.logp_norm, norms, 8ull * n);
+  std::memcpy(o.length, lens, 4ull * n);
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t L = std::min(lens[i], st.T);
+    std::memcpy(o.tokens + (uint64_t)i * o.token_stride, toks + (uint64_t)i * st.T, 4ull * L);
+  }
+  o.count = n;
+  o.status = FT_OK;
+  if (o.step_stats) {
+    const uint64_t* ss = (const uint64_t*)(ob + step_stats_offset(st.F, st.T));
+    std::memcpy(o.step_stats, ss, 8ull * kStepStats * st.T);
+  }
+  return FT_OK;
+}
+
 // Fills `res` from the output blocks of a batch copied back to h_out
 // (out_stride bytes per request).  Returns the first request error.
 static int unpack_results(const uint8_t* h_out, uint64_t out_stride, const StagedReq* staged,
@@ -1333,74 +1396,13 @@ static int unpack_results(const uint8_t* h_out, uint64_t out_stride, const Stage
   ft_timing tm{};
   tm.kernel_ms = kernel_ms;
   const double tick_ms = wall_khz > 0 ? 1.0 / wall_khz : 0.0;
+  std::string msg;
   for (size_t r = 0; r < batch; ++r) {
-    const StagedReq& st = staged[r];
-    ft_result& o = res[r];
-    if (!launched[r]) {
-      // staged but not launched since: d_out holds no result of this request
-      o.count = 0;
-      o.status = FT_E_STATE;
-      if (!first_err) {
-        first_err = FT_E_STATE;
-        g_err = "request " + std::to_string(r) + ": staged but not launched";
-      }
-      continue;
-    }
-    if (st.skip) {
-      o.count = 0;
-      o.status = FT_OK;
-      continue;
-    }
-    const uint8_t* ob = h_out + out_stride * r;
-    const OutHeader* oh = (const OutHeader*)ob;
-    tm.expand_ms += oh->ticks_expand * tick_ms;
-    tm.select_ms += oh->ticks_select * tick_ms;
-    tm.other_ms += (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
-    tm.candidates += oh->candidates;
-    tm.parents += oh->parents;
-    tm.children += oh->children;
-    tm.probes += oh->probes;
-    if (oh->status) {
-      o.count = 0;
-      o.status = (oh->status & kStatusHistory) ? FT_E_LIMIT : FT_E_KERNEL;
-      if (!first_err) {
-        first_err = o.status;
-        g_err = "request " + std::to_string(r) +
-                ((oh->status & kStatusHistory)    ? ": hypotheses exceed max_num_inter_beams"
-                 : (oh->status & kStatusNotReady) ? ": its staged data was not ready in time"
-                                                  : ": kernel status " + std::to_string(oh->status));
-      }
-      continue;
-    }
-    const uint32_t n = oh->count;
-    if (n > o.capacity || (n && (!o.logp_norm || !o.length || !o.tokens)) ||
-        o.token_stride < st.T) {
-      o.count = 0;
-      o.status = FT_E_ARG;
-      if (!first_err) {
-        first_err = FT_E_ARG;
-        g_err = "request " + std::to_string(r) + ": result arrays too small";
-      }
-      continue;
-    }
-    o.device_ms[0] = oh->ticks_expand * tick_ms;
-    o.device_ms[1] = oh->ticks_select * tick_ms;
-    o.device_ms[2] = (double)(oh->ticks_total - oh->ticks_expand - oh->ticks_select) * tick_ms;
-    o.device_ms[3] = oh->ticks_total * tick_ms;
-    const double* norms = (const double*)(ob + sizeof(OutHeader));
-    const uint32_t* lens = (const uint32_t*)(norms + st.F);
-    const uint32_t* toks = lens + st.F;
-    std::memcpy(o.logp_norm, norms, 8ull * n);
-    std::memcpy(o.length, lens, 4ull * n);
-    for (uint32_t i = 0; i < n; ++i) {
-      const uint32_t L = std::min(lens[i], st.T);
-      std::memcpy(o.tokens + (uint64_t)i * o.token_stride, toks + (uint64_t)i * st.T, 4ull * L);
-    }
-    o.count = n;
-    o.status = FT_OK;
-    if (o.step_stats) {
-      const uint64_t* ss = (const uint64_t*)(ob + step_stats_offset(st.F, st.T));
-      std::memcpy(o.step_stats, ss, 8ull * kStepStats * st.T);
+    const int rc = unpack_one(h_out + out_stride * r, staged[r], launched[r] != 0, r, res[r],
+                              tick_ms, tm, &msg);
+    if (rc && !first_err) {
+      first_err = rc;
+      g_err = msg;
     }
   }
   if (timing) *timing = tm;
@@ -1456,11 +1458,18 @@ void pack_stream(PackJob& j, std::pair<uint32_t, uint32_t>* tmp) {
 // ready word is written, copies the packed block to the device itself and
 // writes the results back to mapped host memory, so packing overlaps the
 // launch and the search of the requests before it, and no copy engine sits
-// on the path.  Errors are those of ft_stage + ft_launch + ft_fetch: a
-// request that fails to pack is withdrawn (with every later one), the
-// kernel is waited for, and the first error in request order is returned.
+// on the path.  Each request's results are taken (and handed to `fn`) as
+// soon as its leader publishes them, while the others still search.
+// Errors are those of ft_stage + ft_launch + ft_fetch: a request that fails
+// to pack is withdrawn, the kernel is waited for, and the first error in
+// request order is returned.
 int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
               ft_result* results, ft_timing* timing) {
+  return ft_search_each(c, reqs, batch, results, timing, nullptr, nullptr);
+}
+
+int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* results,
+                   ft_timing* timing, ft_result_fn fn, void* user) {
   if (!c || (!reqs && batch) || (!results && batch))
     return fail(FT_E_ARG, "ft_search: null argument");
   if (!c->reserved) return fail(FT_E_STATE, "ft_search: init_tbs_gpu (ft_reserve) was not called");
@@ -1472,6 +1481,9 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
     int rc = ft_stage(c, reqs, batch);
     if (!rc) rc = ft_launch(c);
     if (!rc) rc = ft_fetch(c, results, batch, timing);
+    if (fn && rc != FT_E_ARG)
+      for (size_t r = 0; r < batch; ++r)
+        if (results[r].status == FT_OK) fn(user, r);
     return rc;
   }
   (void)hipSetDevice(c->device);
@@ -1514,6 +1526,9 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
   a.ready = c->m_ready;
   a.out_host = c->m_out;
   a.stage_bytes = used;
+  // the result headers start unpublished
+  for (size_t r = 0; r < batch; ++r)
+    __atomic_store_n(&((OutHeader*)(c->h_out + c->out_stride * r))->status, 0u, __ATOMIC_RELAXED);
   if (int rc = launch_timed(c, a)) return drop(rc);
   PackJob job;
   job.reqs = reqs;
@@ -1526,17 +1541,71 @@ int ft_search(ft_ctx* c, const ft_request* reqs, size_t batch,
   job.rc.assign(batch, FT_OK);
   job.msg.resize(batch);
   pack_stream(job, c->sort_tmp.data());
+  // Each request's results once its leader has published them (kStatusDone
+  // in its header, written last with a system-scope release), in the order
+  // the requests finish; the stream is looked at now and then, so that a
+  // kernel that ends without publishing one is noticed.
+  ft_timing tm{};
+  const double tick_ms = c->wall_khz > 0 ? 1.0 / c->wall_khz : 0.0;
+  std::vector<int>& rcs = c->req_rc;
+  std::vector<std::string>& msgs = c->req_msg;
+  rcs.assign(batch, FT_OK);
+  if (msgs.size() < batch) msgs.resize(batch);
+  std::vector<uint8_t>& got = c->req_got;
+  got.assign(batch, 0);
+  size_t left = batch;
+  auto take = [&](size_t r) {
+    got[r] = 1;
+    --left;
+    if (job.rc[r]) return;  // withdrawn: its packing error is reported
+    rcs[r] = unpack_one(c->h_out + c->out_stride * r, c->staged[r], true, r, results[r], tick_ms,
+                        tm, &msgs[r]);
+    if (rcs[r] == FT_OK && fn) fn(user, r);
+  };
+  for (size_t r = 0; r < batch; ++r)
+    if (c->staged[r].skip) take(r);
+  bool over = false;
+  for (uint32_t it = 1; left; ++it) {
+    for (size_t r = 0; r < batch; ++r) {
+      if (got[r]) continue;
+      const uint32_t* sw = &((const OutHeader*)(c->h_out + c->out_stride * r))->status;
+      if (__atomic_load_n(sw, __ATOMIC_ACQUIRE) & kStatusDone) take(r);
+    }
+    if (!left) break;
+    if (over) {  // the kernel ended and these were never published
+      for (size_t r = 0; r < batch; ++r)
+        if (!got[r]) {
+          got[r] = 1;
+          rcs[r] = FT_E_KERNEL;
+          msgs[r] = "request " + std::to_string(r) + ": the search ended without its results";
+          results[r].count = 0;
+          results[r].status = FT_E_KERNEL;
+        }
+      break;
+    }
+    if ((it & 63u) == 0) {
+      const hipError_t q = hipStreamQuery(c->stream);
+      if (q == hipSuccess) {
+        over = true;  // one more look at the headers, then give up
+      } else if (q != hipErrorNotReady) {
+        (void)hipStreamSynchronize(c->stream);
+        return drop(hip_fail(q, "search kernel"));
+      }
+    }
+    _mm_pause();
+  }
   double ms = 0.0;
   if (int rc = ft_sync(c, &ms)) return drop(rc);
-  for (size_t r = 0; r < batch; ++r)  // the first packing error in request order
-    if (job.rc[r]) return drop(fail(job.rc[r], job.msg[r]));
-  for (size_t r = 0; r < batch; ++r) c->launched_slot[r] = 1;
-  const int rc = unpack_results(c->h_out, c->out_stride, c->staged.data(),
-                                c->launched_slot.data(), batch, results, c->wall_khz, ms, timing);
+  tm.kernel_ms = ms;
+  if (timing) *timing = tm;
   // the results were taken here: d_out holds no batch for ft_fetch
   c->staged.clear();
   c->launched_slot.clear();
-  return rc;
+  for (size_t r = 0; r < batch; ++r)  // the first packing error in request order
+    if (job.rc[r]) return fail(job.rc[r], job.msg[r]);
+  for (size_t r = 0; r < batch; ++r)
+    if (rcs[r]) return fail(rcs[r], msgs[r]);
+  return FT_OK;
 }
 
 // Host side of the no-allocation path: pageable buffers in the library's

@@ -44,10 +44,7 @@ void require_trie(const TrieImpl* t) {
 // Shape checks shared by the host and device paths.  The step count is the
 // number of topk_logp rows (louds-trie.cc:143) and K the length of row 0
 // (louds-trie.cc:120-123).
-struct Shape {
-  size_t T = 0, K = 0;
-  UInt32 F = 0;
-};
+using Shape = TbsShape;
 
 Shape check_shape(const TbsInput& in) {
   Shape s;
@@ -342,19 +339,18 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
   if (inputs.size() > t.max_batch)
     throw Exception(MARISA_BOUND_ERROR, "tbs_gpu_batched: batch larger than max_batch_size");
   const size_t B = inputs.size();
-  std::vector<ft_request> reqs(B);
-  std::vector<ft_result> res(B);
-  std::vector<std::vector<const uint32_t*>> idrows(B);
-  std::vector<std::vector<const float*>> lprows(B);
-  std::vector<Shape> shapes(B);
-  // result arrays, left uninitialised: the search writes the first count
-  // entries of each, and only those are read
-  std::vector<std::unique_ptr<double[]>> norms(B);
-  std::vector<std::unique_ptr<uint32_t[]>> lens(B), toks(B);
+  // one search at a time per trie; its request and result buffers are kept
+  // from call to call
+  std::lock_guard<std::mutex> lock(t.search_mu);
+  TrieImpl::SearchBuffers& sb = t.sb;
+  sb.reqs.resize(B);
+  sb.res.resize(B);
+  sb.shapes.resize(B);
+  if (sb.rows.size() < B) sb.rows.resize(B);
   for (size_t b = 0; b < B; ++b) {
     const TbsInput& in = inputs[b];
-    shapes[b] = check_shape(in);
-    ft_request& q = reqs[b];
+    sb.shapes[b] = check_shape(in);
+    ft_request& q = sb.reqs[b];
     std::memset(&q, 0, sizeof(q));
     q.beams = in.beams.data();
     q.num_beams = (uint32_t)in.beams.size();
@@ -362,50 +358,58 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
     q.sent_logp_threshold = in.sent_logp_threshold;
     q.length_norm = in.length_norm;
     q.early_exit = in.early_exit ? 1 : 0;
-    std::memset(&res[b], 0, sizeof(ft_result));
-    if (shapes[b].F == 0) continue;
-    const size_t T = shapes[b].T, K = shapes[b].K;
+    std::memset(&sb.res[b], 0, sizeof(ft_result));
+    if (sb.shapes[b].F == 0) continue;
+    const size_t T = sb.shapes[b].T, K = sb.shapes[b].K;
     q.num_steps = (uint32_t)T;
     q.topk = (uint32_t)K;
-    idrows[b].resize(T);
-    lprows[b].resize(T);
+    TrieImpl::SearchBuffers::Rows& rw = sb.rows[b];
+    rw.id.resize(T);
+    rw.lp.resize(T);
     for (size_t r = 0; r < T; ++r) {
-      idrows[b][r] = in.topk_id[r].data();
-      lprows[b][r] = in.topk_logp[r].data();
+      rw.id[r] = in.topk_id[r].data();
+      rw.lp[r] = in.topk_logp[r].data();
     }
-    q.topk_id_rows = idrows[b].data();
-    q.topk_logp_rows = lprows[b].data();
-    const size_t F = shapes[b].F;
-    norms[b].reset(new double[F]);
-    lens[b].reset(new uint32_t[F]);
-    toks[b].reset(new uint32_t[F * T]);
-    res[b].capacity = (uint32_t)F;
-    res[b].token_stride = (uint32_t)T;
-    res[b].logp_norm = norms[b].get();
-    res[b].length = lens[b].get();
-    res[b].tokens = toks[b].get();
+    q.topk_id_rows = rw.id.data();
+    q.topk_logp_rows = rw.lp.data();
+    // result arrays, grown as needed and never shrunk: the search writes the
+    // first count entries of each, and only those are read
+    const size_t F = sb.shapes[b].F;
+    if (rw.norms.size() < F) rw.norms.resize(F);
+    if (rw.lens.size() < F) rw.lens.resize(F);
+    if (rw.toks.size() < F * T) rw.toks.resize(F * T);
+    ft_result& o = sb.res[b];
+    o.capacity = (uint32_t)F;
+    o.token_stride = (uint32_t)T;
+    o.logp_norm = rw.norms.data();
+    o.length = rw.lens.data();
+    o.tokens = rw.toks.data();
   }
-  int rc;
-  {
-    std::lock_guard<std::mutex> lock(t.search_mu);
-    rc = ft_search(t.ctx, reqs.data(), B, res.data(), nullptr);
-  }
-  if (rc) throw_ft(rc, "tbs_gpu_batched");
-  for (size_t b = 0; b < B; ++b) {
-    TbsInput& in = inputs[b];
-    if (shapes[b].F == 0) continue;  // outputs untouched
-    const ft_result& o = res[b];
-    const size_t T = shapes[b].T;
+  // each request's output vectors are filled as soon as its results are
+  // in, while the rest of the batch still searches
+  struct Fill {
+    std::vector<TbsInput>* inputs;
+    TrieImpl::SearchBuffers* sb;
+  } fill{&inputs, &sb};
+  auto on_result = [](void* user, size_t b) {
+    Fill& f = *(Fill*)user;
+    TbsInput& in = (*f.inputs)[b];
+    if (f.sb->shapes[b].F == 0) return;  // outputs untouched
+    const ft_result& o = f.sb->res[b];
+    const size_t T = f.sb->shapes[b].T;
+    const TrieImpl::SearchBuffers::Rows& rw = f.sb->rows[b];
     in.out_sent.resize(o.count);
-    in.out_logp_norm.assign(norms[b].get(), norms[b].get() + o.count);
+    in.out_logp_norm.assign(rw.norms.data(), rw.norms.data() + o.count);
     for (uint32_t i = 0; i < o.count; ++i)
-      in.out_sent[i].assign(toks[b].get() + i * T, toks[b].get() + i * T + lens[b][i]);
+      in.out_sent[i].assign(rw.toks.data() + i * T, rw.toks.data() + i * T + rw.lens[i]);
     in.t_expansion_ms = o.device_ms[0];
     in.t_validation_ms = 0.0;
     in.t_selection_ms = o.device_ms[1];
     in.t_grid_overhead_ms = o.device_ms[2];
     in.kernel_ms = o.device_ms[3];
-  }
+  };
+  const int rc = ft_search_each(t.ctx, sb.reqs.data(), B, sb.res.data(), nullptr, on_result, &fill);
+  if (rc) throw_ft(rc, "tbs_gpu_batched");
 }
 
 std::size_t Trie::num_tries() const {

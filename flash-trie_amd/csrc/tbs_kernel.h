@@ -23,6 +23,9 @@ enum : uint32_t {
   kStatusWithdrawn = 8u, // streamed search: the host withdrew the request
   kStatusNotReady = 16u, // streamed search: its ready word never came
   kStatusStage = 32u,    // streamed search: the packed block is out of bounds
+  // streamed search: set in the status word of a request's header in host
+  // memory, written last (a system-scope release): its results are there
+  kStatusDone = 0x80000000u,
 };
 
 // Streamed search: the ready word of a request, (launch epoch << 32) | state,

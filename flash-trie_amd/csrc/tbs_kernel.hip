@@ -1257,9 +1257,11 @@ __device__ __forceinline__ uint32_t stage_in(const KArgs& a, uint32_t req, uint8
       st_dev(&((Ctl*)(ws + a.lay.ctl))->go, tag | kGoExit);
       OutHeader* oh = (OutHeader*)(a.out_host + (uint64_t)req * a.out_stride);
       oh->count = 0;
-      oh->status = v == (tag | kReadyWithdrawn) ? kStatusWithdrawn
-                   : v == (tag | kReadyOk)      ? kStatusStage
-                                                : kStatusNotReady;
+      const uint32_t st = v == (tag | kReadyWithdrawn) ? kStatusWithdrawn
+                          : v == (tag | kReadyOk)      ? kStatusStage
+                                                       : kStatusNotReady;
+      __hip_atomic_store(&oh->status, st | kStatusDone, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
     }
     return kStageFailed;
   }
@@ -2461,10 +2463,13 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     const uint64_t* ss = (const uint64_t*)(ob + so);
     uint64_t* hs = (uint64_t*)(rb + so);
     for (uint32_t i = tid; i < d.out_T * kStepStats; i += kBlock) hs[i] = ss[i];
+    // every thread's results have reached host memory before the header
+    // says so (below)
+    wait_stores();
+    __syncthreads();
   }
   if (tid == 0) {
     oh->count = status ? 0 : nS;
-    oh->status = status;
     const unsigned long long tend = wall_clock64();
     oh->ticks_expand = t_exp;
     oh->ticks_select = t_sel;
@@ -2473,6 +2478,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     oh->parents = sm.cnt_parents;
     oh->children = sm.cnt_children;
     oh->probes = sm.cnt_probes;
+    if constexpr (kStreamed) {
+      // published last: the host takes the request's results as soon as it
+      // sees kStatusDone, while other requests may still be searching
+      __hip_atomic_store(&oh->status, status | kStatusDone, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    } else {
+      oh->status = status;
+    }
   }
 }
 

@@ -207,6 +207,19 @@ int ft_fetch(ft_ctx* ctx, ft_result* results, size_t batch,
 int ft_search(ft_ctx* ctx, const ft_request* reqs, size_t batch,
               ft_result* results, ft_timing* timing);
 
+/* ft_search that hands each request's results over as soon as they are
+ * there: fn(user, r) is called (on the calling thread) once results[r] is
+ * filled and its status is FT_OK -- for a streamed search as each
+ * request's leader finishes, while other requests of the batch may still
+ * be searching -- so a caller can convert results while the rest run.  No
+ * counterpart in the reference; it is what Trie::tbs_gpu_batched calls.
+ * Return value, errors and results are those of ft_search (fn is not
+ * called for a request with an error). */
+typedef void (*ft_result_fn)(void* user, size_t r);
+int ft_search_each(ft_ctx* ctx, const ft_request* reqs, size_t batch,
+                   ft_result* results, ft_timing* timing, ft_result_fn fn,
+                   void* user);
+
 /* ft_search without allocating: no hipMalloc, hipHostMalloc or hipFree,
  * and no ft_reserve needed.  It has no counterpart in the reference; it is
  * for callers that cannot allocate (code under HIP graph capture, tight

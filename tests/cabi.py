@@ -32,6 +32,10 @@ class Result(ctypes.Structure):
                 ("step_stats", ctypes.POINTER(ctypes.c_uint64))]
 
 
+# ft_result_fn: void (*)(void* user, size_t r)
+RESULT_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_size_t)
+
+
 def load():
     lib = ctypes.CDLL(LIB)
     lib.ft_create.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
@@ -42,6 +46,10 @@ def load():
             getattr(lib, name).argtypes = [ctypes.c_void_p, ctypes.POINTER(Request),
                                            ctypes.c_size_t, ctypes.POINTER(Result),
                                            ctypes.c_void_p]
+    if hasattr(lib, "ft_search_each"):
+        lib.ft_search_each.argtypes = [ctypes.c_void_p, ctypes.POINTER(Request),
+                                       ctypes.c_size_t, ctypes.POINTER(Result),
+                                       ctypes.c_void_p, RESULT_FN, ctypes.c_void_p]
     lib.ft_stage.argtypes = [ctypes.c_void_p, ctypes.POINTER(Request), ctypes.c_size_t]
     lib.ft_launch_range.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t]
     lib.ft_fetch.argtypes = [ctypes.c_void_p, ctypes.POINTER(Result), ctypes.c_size_t,

@@ -48,6 +48,62 @@ def test_c_abi_search_through_ctypes(ft, po):
 
 
 @pytest.mark.gpu
+def test_search_each_hands_over_every_request(ft, po):
+    """ft_search_each calls back once for every request whose results are
+    complete -- the results are already the oracle's when the callback
+    runs -- and not for a request that fails to pack (whose error the call
+    returns); a request with final beam 0 is handed over with no results."""
+    lib = load()
+    from cabi import RESULT_FN
+    toks, offs = ft.synth_keys(30000, 4096, 3, 8, 1.1, 22)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    image = np.array(t.image(), dtype=np.uint8)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    B, T, K, F, n = 16, 8, 32, 16, 8
+    ids, lp = ft.synth_requests(t, 0, n, 4096, T, K, B, 0.3, 2.0, True, 22, model=1)
+    beams = np.full((n, T), B, dtype=np.uint32)
+    beams[3, T - 1] = 0  # final beam 0: outputs untouched (louds-trie.cc:114-117)
+    lp = lp.copy()
+    ctx = ctypes.c_void_p()
+    check(lib, lib.ft_create(image.ctypes.data, image.nbytes, 0, ctypes.byref(ctx)))
+    try:
+        check(lib, lib.ft_reserve(ctx, n, K, T, B, B * T, 4096))
+        for bad in (None, 5):
+            lpx = lp.copy()
+            if bad is not None:
+                lpx[bad, 2, 7] = np.nan
+            b = Batch(beams, ids, lpx, -10.0, -40.0, 5.0, False, F)
+            seen, at_call = [], {}
+
+            def on_result(user, r):
+                seen.append(r)
+                at_call[r] = (b.res[r].status, b.results(r))
+
+            cb = RESULT_FN(on_result)
+            print("ctypes ft_search_each batch", n, "bad", bad, flush=True)
+            rc = lib.ft_search_each(ctx, b.reqs, n, b.res, None, cb, None)
+            want_seen = [r for r in range(n) if r != bad]
+            assert sorted(seen) == want_seen, seen
+            if bad is None:
+                assert rc == 0, lib.ft_last_error()
+            else:
+                assert rc == -6, rc  # FT_E_INPUT, naming the request
+                assert f"request {bad}" in lib.ft_last_error().decode()
+            for r in want_seen:
+                status, (seqs, norms) = at_call[r]
+                assert status == 0
+                if r == 3:
+                    assert seqs == [], seqs
+                    continue
+                want = o.tbs(beams[r], ids[r], lpx[r], -10.0, -40.0, 5.0, False)
+                assert seqs == want[0], r
+                assert np.array_equal(norms, want[1]), r
+    finally:
+        lib.ft_destroy(ctx)
+
+
+@pytest.mark.gpu
 def test_second_process_searches_after_this_one(ft, tmp_path):
     # launches are ordinary (no cooperative launch), so a second process can
     # search on the GPU while this one, which has searched already, lives
