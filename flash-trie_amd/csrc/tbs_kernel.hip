@@ -64,6 +64,11 @@ constexpr uint32_t kRowHashEmpty = 0xFFFFFFFFu;
 // the leader hashes the row for steps of at least this many work items (a
 // smaller step does too few lookups to repay the build)
 constexpr uint32_t kRowHashMinWork = 2048;
+// the single-wave tail: at most this many steps' rows in LDS per round,
+// and the bits that mark a token its row does not hold (a NaN, which no
+// staged logp is)
+constexpr uint32_t kTailMaxRows = 32;
+constexpr uint32_t kAbsent = 0xFFFFFFFFu;
 
 struct alignas(16) Smem {
   // counters, flags and small arrays first: their LDS addresses fit the
@@ -87,7 +92,7 @@ struct alignas(16) Smem {
   uint16_t stolen[256];
   uint32_t multi_item;  // some parent of the step has other than one item
   // the single-wave tail (tiny steps): where it stopped, for every thread
-  uint32_t tiny_t, tiny_ncur, tiny_nS, tiny_hist, tiny_done;
+  uint32_t tiny_t, tiny_ncur, tiny_nS, tiny_hist, tiny_done, tiny_handback;
   unsigned long long tiny_cands, tiny_ticks;
   uint32_t par_w;       // work items of a step with at most 64 parents
   uint32_t w_children, w_probes;
@@ -136,6 +141,19 @@ struct alignas(16) Smem {
     };
     // selection: wide histogram (done before keep_idx is filled)
     uint32_t whist[kWideBins];
+    // the single-wave tail, per round of steps whose rows are in LDS: the
+    // pending token of hypothesis (lane) j at the round's step r in
+    // tl_tok[r * 64 + j] (kNoToken where it is not read ahead), the bits of
+    // its logp in that step's row in tl_x[r * 64 + j] (kAbsent when the
+    // row does not hold it), the steps' beam widths, and each hypothesis's
+    // last token and parent record between rounds
+    struct {
+      uint32_t tl_tok[(kTailMaxRows + 1) * 64];
+      uint32_t tl_x[kTailMaxRows * 64];
+      uint32_t tl_beams[kTailMaxRows];
+      uint32_t tl_rtok[64];
+      uint32_t tl_rphist[64];
+    };
   };
   // expansion: this workgroup's pushes, appended to the request's lists at
   // the end of its share of the step
@@ -1434,21 +1452,94 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
   }
 }
 
-// The single-wave tail of a request's search (see the leader's step loop):
-// wave 0 of the leader, lane j holding hypothesis j (j < n_cur) of a beam
-// of link parents whose parent table for step t0 is in LDS, and row t0 in
-// LDS.  Runs steps t0, t0 + 1, ... while every push survives: the
-// hypothesis's pending key token is looked up in the row, thresholds
-// applied (louds-trie.cc:87-90), and the extension goes to `selected` when
-// it completes the key (louds-trie.cc:97-102), else stays a link parent in
-// `next`.  Survivors keep their lanes (ranks among the live lanes give
-// their beam and history positions); the next row is read into registers
-// during a step and written to LDS at its end.  Stops (sm.tiny_done) when
-// the beam empties, the steps run out, or early exit fills `selected`; or
-// hands back (sm.tiny_done = 0) at the first step whose pushes overflow a
+// The single-wave tail of a request's search (see the leader's step loop)
+// runs in rounds of up to kTailMaxRows steps.  Each round the whole leader
+// workgroup reads the rows of the round's steps into LDS (tail_fill),
+// with the steps' beam widths and each hypothesis's pending tokens of those
+// steps; then wave 0 runs the steps (tiny_steps) with no global read on its
+// path, so that a step costs its LDS searches and stores rather than a
+// memory round trip.
+//
+// tail_fill: rows t .. t + nr - 1 into the LDS row arrays (row r at
+// r * Kp), their beam widths into tl_beams, and, for each hypothesis j <
+// n_cur of the LDS parent table whose pending token of step t is on its
+// node's own edge (tail index tc), the tokens of steps t + r, r = 1 .. nr,
+// that come before its key ends (string depth sd: steps < sd), tail[tc + r]
+// -- the entries the hypothesis reads if it survives; then every token so
+// known is searched in its row (tl_x).  Every thread; the caller
+// synchronises afterwards.
+__device__ __forceinline__ void tail_fill(const KArgs& a, const uint32_t* rid, const float* rlp,
+                                          const uint32_t* beams, uint32_t t, uint32_t nr,
+                                          uint32_t K, uint32_t Kp, uint32_t n_cur, Smem& sm) {
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t r0 = 0; r0 < nr; r0 += 4u) {
+    uint32_t id[4];
+    float lp[4];
+#pragma unroll
+    for (uint32_t u = 0; u < 4u; ++u) {
+      const uint32_t r = r0 + u;
+      if (r < nr && tid < K) {
+        const uint64_t o = (uint64_t)(t + r) * K + tid;
+        id[u] = rid[o];
+        lp[u] = rlp[o];
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 4u; ++u) {
+      const uint32_t r = r0 + u;
+      if (r < nr && tid < K) {
+        sm.row_id[r * Kp + tid] = id[u];
+        sm.row_lp[r * Kp + tid] = lp[u];
+      }
+    }
+  }
+  if (tid < nr) sm.tl_beams[tid] = beams[t + tid];
+  for (uint32_t i = tid; i < (nr + 1u) * 64u; i += kBlock) {
+    const uint32_t r = i >> 6, j = i & 63u;
+    uint32_t tok = kNoToken;
+    if (r > 0 && j < n_cur) {
+      const uint32_t tc = sm.p_lp[j];
+      if (tc != kNoCursor && t + r < sm.p_c0[j]) tok = a.tail[tc + r];
+    }
+    sm.tl_tok[i] = tok;
+  }
+  __syncthreads();
+  // each known pending token in its step's row (binary search): its logp's
+  // bits, or kAbsent -- the searches of the whole round at once, one per
+  // thread, instead of one after another on wave 0
+  for (uint32_t i = tid; i < nr * 64u; i += kBlock) {
+    const uint32_t r = i >> 6, j = i & 63u;
+    uint32_t xb = kAbsent;
+    const uint32_t tok = j >= n_cur ? kNoToken : r == 0 ? sm.p_aux[j] : sm.tl_tok[i];
+    if (tok != kNoToken) {
+      const uint32_t rb = r * Kp;
+      uint32_t lo = 0, hi = K;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (sm.row_id[rb + mid] < tok) lo = mid + 1; else hi = mid;
+      }
+      if (lo < K && sm.row_id[rb + lo] == tok) xb = __float_as_uint(sm.row_lp[rb + lo]);
+    }
+    sm.tl_x[i] = xb;
+  }
+}
+
+// tiny_steps: wave 0 of the leader, lane j holding hypothesis j (j < n_cur)
+// of a beam of link parents whose parent table for step t is in LDS, runs
+// steps t .. t + nr - 1 on the rows tail_fill put there while every push
+// survives: the hypothesis's pending key token is looked up in the row,
+// thresholds applied (louds-trie.cc:87-90), and the extension goes to
+// `selected` when it completes the key (louds-trie.cc:97-102), else stays a
+// link parent in `next`.  Survivors keep their lanes (ranks among the live
+// lanes give their beam and history positions).  Stops (sm.tiny_done) when
+// the beam empties, the steps run out, or early exit fills `selected`;
+// hands back (sm.tiny_handback) at the first step whose pushes overflow a
 // heap (bounded selection), would cut `selected` under early exit, or hit
 // a capacity limit -- then the beam is written to cur and the LDS / global
-// parent table of that step, which the general step reruns from scratch.
+// parent table of that step, which the general step reruns from scratch;
+// else, after nr steps, leaves the beam in the LDS parent table (and each
+// hypothesis's history links in tl_rtok / tl_rphist) for the next round
+// (`first` is false there).
 // A value every lane of the wave holds alike, marked so: what is derived
 // from it can live in scalar registers rather than vector ones.
 __device__ __forceinline__ uint32_t uni(uint32_t x) {
@@ -1461,17 +1552,12 @@ __device__ __forceinline__ float uni(float x) { return __uint_as_float(uni(__flo
 __device__ __forceinline__ double uni(double x) {
   return __longlong_as_double((long long)uni((uint64_t)__double_as_longlong(x)));
 }
-// second row buffer of the tiny steps, inside the LDS row arrays (rows of
-// at most kBlock proposals)
-constexpr uint32_t kTinyRowBuf = kBlock;
-static_assert(2 * kTinyRowBuf <= kMaxLdsTopk, "two tiny-step row buffers fit the LDS row");
 
 __device__ __forceinline__ void tiny_steps(
-    const KArgs& a, const DevReq& d, uint32_t t, uint32_t n_cur, uint32_t nS,
-    uint32_t hist_used, uint32_t lane, const double* lnf, const uint32_t* beams,
-    const uint32_t* rid, const float* rlp, CurRec* cur, SelRec* selA, HistRec* hist,
-    uint32_t* par_c0, uint32_t* par_aux, uint32_t* par_node, uint32_t* par_mode,
-    uint64_t* step_stats, Smem& sm) {
+    const KArgs& a, const DevReq& d, uint32_t t, uint32_t nr, uint32_t Kp, bool first,
+    uint32_t n_cur, uint32_t nS, uint32_t hist_used, uint32_t lane, const double* lnf,
+    CurRec* cur, SelRec* selA, HistRec* hist, uint32_t* par_c0, uint32_t* par_aux,
+    uint32_t* par_node, uint32_t* par_mode, uint64_t* step_stats, Smem& sm) {
   const uint32_t T = d.T, K = d.K, F = d.F;
   const bool early = (d.flags & kReqEarlyExit) != 0;
   const uint64_t lt = (1ull << lane) - 1ull;
@@ -1482,6 +1568,8 @@ __device__ __forceinline__ void tiny_steps(
   // record, the links of the record a step below adds
   uint32_t rtok = 0, rphist = kNoHist;
   double s = 0.0;
+  // its pending tokens of this round are in tl_tok (it is on its own edge)
+  bool ahead = false;
   if (alive) {
     node = sm.p_node[lane];
     s = sm.p_s[lane];
@@ -1490,49 +1578,45 @@ __device__ __forceinline__ void tiny_steps(
     sd = sm.p_c0[lane];
     ptok = sm.p_aux[lane];
     tc = sm.p_lp[lane];
-    if (hst < a.lay.hist_cap) {
+    ahead = tc != kNoCursor;
+    if (!first) {
+      rtok = sm.tl_rtok[lane];
+      rphist = sm.tl_rphist[lane];
+    } else if (hst < a.lay.hist_cap) {
       const HistRec r = hist[hst];
       rtok = r.tok;
       rphist = r.phist;
     }
   }
   uint32_t status = 0;
-  bool done = false;
+  bool done = false, handback = false;
   unsigned long long cands = 0, ticks = 0;
-  constexpr int kPf = kBlock / 64;  // row entries per lane
-  uint32_t cb = 0;  // row buffer of the current step: row_id / row_lp + cb
-  for (; t < T; ++t) {
+  // one clock read per step: the end of a step is the start of the next
+  unsigned long long c0 = wall_clock64();
+  for (uint32_t r = 0; r < nr; ++r, ++t) {
     if (n_cur == 0 || (early && nS >= F)) {
       done = true;
       break;
     }
-    const unsigned long long c0 = wall_clock64();
-    const bool more = t + 1 < T;
-    // the next row straight into the other LDS row buffer (no registers),
-    // while this step searches its own
-    const uint32_t nb = kTinyRowBuf - cb;
-    if (more) {
-      const uint64_t ro = (uint64_t)(t + 1) * K;
-#pragma unroll
-      for (int i = 0; i < kPf; ++i) {
-        const uint32_t k = min((uint32_t)i * 64u + lane, K - 1u);
-        __builtin_amdgcn_global_load_lds(rid + ro + k, &sm.row_id[nb + (uint32_t)i * 64u], 4, 0, 0);
-        __builtin_amdgcn_global_load_lds(rlp + ro + k, &sm.row_lp[nb + (uint32_t)i * 64u], 4, 0, 0);
-      }
-    }
-    // the pending token in the row, thresholds in double (`<=` drops)
+    // the pending token in the row (searched by tail_fill when the token
+    // was known there), thresholds in double (`<=` drops)
     bool pass = false;
     double s2 = 0.0;
-    int pos = -1;
     if (alive) {
-      uint32_t lo = 0, hi = K;
-      while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (sm.row_id[cb + mid] < ptok) lo = mid + 1; else hi = mid;
+      uint32_t xb = kAbsent;
+      if (r == 0 || ahead) {
+        xb = sm.tl_x[r * 64u + lane];
+      } else {
+        const uint32_t rb = r * Kp;
+        uint32_t lo = 0, hi = K;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (sm.row_id[rb + mid] < ptok) lo = mid + 1; else hi = mid;
+        }
+        if (lo < K && sm.row_id[rb + lo] == ptok) xb = __float_as_uint(sm.row_lp[rb + lo]);
       }
-      pos = (lo < K && sm.row_id[cb + lo] == ptok) ? (int)lo : -1;
-      if (pos >= 0) {
-        const float x = sm.row_lp[cb + (uint32_t)pos];
+      if (xb != kAbsent) {
+        const float x = __uint_as_float(xb);
         pass = !(((double)x <= (double)d.tok_thr) || (s + (double)x <= d.sent_thr));
         s2 = s + (double)x;
       }
@@ -1541,12 +1625,11 @@ __device__ __forceinline__ void tiny_steps(
     const bool to_next = pass && mode == M_LP_NEXT;
     const uint64_t mS = __ballot(to_sel), mN = __ballot(to_next);
     const uint32_t n_new = (uint32_t)__popcll(mS), n_next = (uint32_t)__popcll(mN);
-    const uint32_t Mnext = beams[t];
-    // every push survives and no limit is reached, or hand back (after the
-    // row reads into LDS have landed)
+    const uint32_t Mnext = sm.tl_beams[r];
+    // every push survives and no limit is reached, or hand back
     if (n_next > Mnext || nS + n_new > F || nS + n_new > a.lay.sel_cap ||
         hist_used + n_next > a.lay.hist_cap) {
-      wait_stores();
+      handback = true;
       break;
     }
     // early exit with `selected` exactly full: every new push is among the
@@ -1566,16 +1649,16 @@ __device__ __forceinline__ void tiny_steps(
     if (stop_early) {  // selected is full: the search ends here
       nS += n_new;
       cands += n_new;
+      const unsigned long long c1 = wall_clock64();
       if (lane == 0 && t < d.out_T) {
         uint64_t* row = step_stats + (uint64_t)t * kStepStats;
         row[0] = n_cur;
         row[1] = n_cur;
         row[2] = n_next;
         row[3] = n_new;
-        row[4] = wall_clock64() - c0;
+        row[4] = c1 - c0;
       }
-      ticks += wall_clock64() - c0;
-      wait_stores();
+      ticks += c1 - c0;
       done = true;
       break;
     }
@@ -1592,51 +1675,66 @@ __device__ __forceinline__ void tiny_steps(
       hst = o;
       s = s2;
       // the pending token of step t + 1: on the node's own edge the next
-      // tail token, else the walk parent_entry makes
+      // tail token (read ahead by tail_fill when the round began there),
+      // else the walk parent_entry makes
       if (tc != kNoCursor) {
         ++tc;
-        ptok = a.tail[tc];
+        // Global reads happen on the rare paths only, and each is waited
+        // for inside its own branch (the empty asm statements use the
+        // values there): a wait where the paths join would also wait for
+        // this step's stores, which count in the same counter.  The LDS
+        // read is taken unconditionally and made opaque for the same
+        // reason: as one arm of a select it became a flat load.
+        uint32_t la = sm.tl_tok[(r + 1u) * 64u + lane];
+        asm volatile("" : "+v"(la));
+        if (!ahead) {
+          la = a.tail[tc];
+          asm volatile("" : "+v"(la));
+        }
+        ptok = la;
         mode = (t + 2 == sd) ? M_LP_SEL : M_LP_NEXT;
       } else {
         // (what parent_entry builds for a link parent at step t + 1)
         uint32_t err = 0;
-        const ft_node_rec r = a.recs[node];
-        ptok = kb_token(a, node, r, t + 1, &err);
+        const ft_node_rec rec = a.recs[node];
+        ptok = kb_token(a, node, rec, t + 1, &err);
         if (err) status |= kStatusCorrupt;
         mode = (t + 2 == sd) ? M_LP_SEL : M_LP_NEXT;
-        const uint32_t el = (r.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
-        tc = ((r.meta & FT_META_LINK) && t + 1 + el >= sd) ? r.tail_off + (t + 1 + el - sd)
-                                                           : kNoCursor;
+        const uint32_t el = (rec.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+        tc = ((rec.meta & FT_META_LINK) && t + 1 + el >= sd) ? rec.tail_off + (t + 1 + el - sd)
+                                                             : kNoCursor;
+        asm volatile("" : "+v"(ptok), "+v"(tc), "+v"(status));
       }
     }
     alive = to_next;
+    const unsigned long long c1 = wall_clock64();
     if (lane == 0 && t < d.out_T) {
       uint64_t* row = step_stats + (uint64_t)t * kStepStats;
       row[0] = n_cur;
       row[1] = n_cur;
       row[2] = n_next;
       row[3] = n_new;
-      row[4] = wall_clock64() - c0;
+      row[4] = c1 - c0;
     }
     hist_used += n_next;
     nS += n_new;
     cands += (uint64_t)n_next + n_new;
     if (lane == 0) sm.cnt_parents += n_cur;
     n_cur = n_next;
-    // the next row has landed in the other buffer (and this step's stores
-    // are complete)
-    wait_stores();
-    cb = nb;
-    ticks += wall_clock64() - c0;
+    ticks += c1 - c0;
+    c0 = c1;
     if (status) break;
   }
-  if (t >= T) done = true;
+  // this wave's stores (history, selected, the step profile) are complete
+  // before the block barrier that follows
+  wait_stores();
+  if (!handback && (t >= T || n_cur == 0 || (early && nS >= F))) done = true;
   const uint64_t am = __ballot(alive);
   if (!done && !status) {
-    // hand the beam back: hypothesis of lane j at position rank(j)
+    // the beam for the next round, or handed back to the general step:
+    // hypothesis of lane j at position rank(j)
     if (alive) {
       const uint32_t o = (uint32_t)__popcll(am & lt);
-      st_cur(&cur[o], s, node, hst);
       sm.p_node[o] = node;
       sm.p_s[o] = s;
       sm.p_hist[o] = hst;
@@ -1644,10 +1742,15 @@ __device__ __forceinline__ void tiny_steps(
       sm.p_c0[o] = sd;
       sm.p_aux[o] = ptok;
       sm.p_lp[o] = tc;
-      st_dev(&par_c0[o], sd);
-      st_dev(&par_aux[o], ptok);
-      st_dev(&par_node[o], node);
-      st_dev(&par_mode[o], mode);
+      sm.tl_rtok[o] = rtok;
+      sm.tl_rphist[o] = rphist;
+      if (handback) {
+        st_cur(&cur[o], s, node, hst);
+        st_dev(&par_c0[o], sd);
+        st_dev(&par_aux[o], ptok);
+        st_dev(&par_node[o], node);
+        st_dev(&par_mode[o], mode);
+      }
     }
   }
   if (lane == 0) {
@@ -1656,6 +1759,7 @@ __device__ __forceinline__ void tiny_steps(
     sm.tiny_nS = nS;
     sm.tiny_hist = hist_used;
     sm.tiny_done = done ? 1u : 0u;
+    sm.tiny_handback = handback ? 1u : 0u;
     sm.tiny_cands = cands;
     sm.tiny_ticks = ticks;
     if (status) sm.status |= status;
@@ -1784,34 +1888,43 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // louds-trie.cc:91-102), each step is one row lookup per hypothesis.
     // A link parent either stays one (next) or closes its key (selected),
     // so the beam stays in this form until it empties.  Wave 0 runs these
-    // steps alone, the hypotheses in its lanes' registers, without block
-    // barriers, for as long as every push survives both heaps (no bounded
-    // selection cuts and early exit does not fire mid-step); at the first
-    // step that needs a cut it hands the beam back to the general step.
+    // steps alone, the hypotheses in its lanes' registers, in rounds of as
+    // many steps as the LDS row arrays hold rows (4 at K = 1000; the
+    // workgroup reads them, with the tokens the hypotheses will look up,
+    // before each round), for as long as every push survives both heaps
+    // (no bounded selection cuts and early exit does not fire mid-step); at
+    // the first step that needs a cut it hands the beam back to the general
+    // step.
     if (par_ready && n_cur <= 64u && K <= (uint32_t)kBlock) {
       const uint32_t lane = tid & 63u;
       const uint32_t md0 = lane < n_cur ? (uint32_t)(sm.p_mode[lane] & kModeMask) : (uint32_t)M_LP_NEXT;
       if (__ballot(md0 != M_LP_NEXT && md0 != M_LP_SEL) == 0) {
-        if (row_pf) {
-          if (tid < K) {
-            sm.row_id[tid] = pf_id;
-            sm.row_lp[tid] = pf_lp;
+        // rows K rounded up to whole waves apart
+        const uint32_t Kp = (K + 63u) & ~63u;
+        const uint32_t R = min((uint32_t)kMaxLdsTopk / Kp, kTailMaxRows);
+        bool first = true, finished = false;
+        for (;;) {
+          const uint32_t nr = min(R, T - t);
+          tail_fill(a, rid, rlp, beams, t, nr, K, Kp, n_cur, sm);
+          __syncthreads();
+          if (tid < 64u) tiny_steps(a, d, t, nr, Kp, first, n_cur, nS, hist_used, lane, lnf,
+                                    cur, selA, hist, par_c0, par_aux, par_node, par_mode,
+                                    step_stats, sm);
+          __syncthreads();
+          t = sm.tiny_t;
+          n_cur = sm.tiny_ncur;
+          nS = sm.tiny_nS;
+          hist_used = sm.tiny_hist;
+          n_cands += sm.tiny_cands;
+          t_exp += sm.tiny_ticks;
+          if (sm.tiny_done || sm.status) {
+            finished = true;
+            break;
           }
-        } else {
-          load_row(rid, rlp, t, K, sm);
+          if (sm.tiny_handback) break;
+          first = false;
         }
-        __syncthreads();
-        if (tid < 64u) tiny_steps(a, d, t, n_cur, nS, hist_used, lane, lnf, beams, rid, rlp,
-                                  cur, selA, hist, par_c0, par_aux, par_node, par_mode,
-                                  step_stats, sm);
-        __syncthreads();
-        t = sm.tiny_t;
-        n_cur = sm.tiny_ncur;
-        nS = sm.tiny_nS;
-        hist_used = sm.tiny_hist;
-        n_cands += sm.tiny_cands;
-        t_exp += sm.tiny_ticks;
-        if (sm.tiny_done || sm.status) break;
+        if (finished) break;
         // a cut is due at step t: the general step below runs it, with the
         // beam handed back in the parent table and row t reloaded
         row_pf = false;
