@@ -230,7 +230,61 @@ int main() {
       CHECK(rc1 == FT_E_INPUT, "stream case %d: pack_batch rc %d", c, rc1);
     }
   }
-  std::printf("%d batches packed, %d rejected, %d streamed batches compared, %d failures\n",
-              cases, rejected, streamed, fails);
+  // The row scan's SIMD variants against a scalar restatement (the ones
+  // this host runs): random rows with NaN, +-inf, +-0, ids around 2^31,
+  // equal and descending neighbours, thresholds inside and outside the
+  // range, lengths around the vector widths.
+  int scanned = 0;
+  {
+    struct Variant {
+      const char* name;
+      ScanRowFn fn;
+      bool ok;
+    } vars[] = {{"sse2", scan_row_sse2, true},
+                {"avx2", scan_row_avx2, (bool)__builtin_cpu_supports("avx2")}};
+    std::vector<uint32_t> id(80), oid(80);
+    std::vector<float> lp(80), olp(80);
+    const float specials[] = {NAN, INFINITY, -INFINITY, 0.0f, -0.0f, -1e-30f, 3.5f};
+    for (int c = 0; c < 20000; ++c) {
+      const uint32_t K = (uint32_t)(g() % 70);
+      uint32_t v = (g() % 2) ? 0x7FFFFFF0u : (uint32_t)(g() % 100);
+      for (uint32_t k = 0; k < K; ++k) {
+        v += (uint32_t)(g() % 3);  // 0: an equal neighbour
+        id[k] = (g() % 50 == 0) ? v - 5u : v;
+        lp[k] = (g() % 25 == 0) ? specials[g() % 7] : -(float)(g() % 80) * 0.25f;
+      }
+      const float thr = (g() % 5 == 0) ? specials[g() % 7] : -(float)(g() % 25);
+      bool bad = false, sorted = true;
+      float lo = INFINITY, hi = -INFINITY;
+      for (uint32_t k = 0; k < K; ++k) {
+        bad = bad || std::isnan(lp[k]) || lp[k] == INFINITY;
+        if (lp[k] > thr) {
+          lo = std::min(lo, lp[k]);
+          hi = std::max(hi, lp[k]);
+        }
+        if (k > 0 && id[k] <= id[k - 1]) sorted = false;
+      }
+      for (const Variant& w : vars) {
+        if (!w.ok) continue;
+        std::fill(oid.begin(), oid.end(), 0u);
+        std::fill(olp.begin(), olp.end(), 0.0f);
+        const RowScan sc = w.fn(id.data(), lp.data(), K, thr, oid.data(), olp.data());
+        CHECK(sc.bad == bad, "scan %s case %d: bad", w.name, c);
+        if (!bad) {
+          CHECK(sc.sorted == sorted, "scan %s case %d: sorted", w.name, c);
+          // +0 and -0 may come out either way; the bounds treat them alike
+          CHECK(sc.lo == lo && sc.hi == hi, "scan %s case %d: lo %g/%g hi %g/%g", w.name, c,
+                sc.lo, lo, sc.hi, hi);
+        }
+        CHECK(std::memcmp(oid.data(), id.data(), 4ull * K) == 0 &&
+                  std::memcmp(olp.data(), lp.data(), 4ull * K) == 0,
+              "scan %s case %d: copy", w.name, c);
+        ++scanned;
+      }
+    }
+  }
+  std::printf("%d batches packed, %d rejected, %d streamed batches compared, %d rows scanned, "
+              "%d failures\n",
+              cases, rejected, streamed, scanned, fails);
   return fails ? 1 : 0;
 }

@@ -21,3 +21,4 @@ def test_packing_matches_scalar_restatement(tmp_path):
     p = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert p.returncode == 0, p.stdout
     assert "0 failures" in p.stdout and "0 streamed" not in p.stdout, p.stdout
+    assert " 0 rows scanned" not in p.stdout, p.stdout
