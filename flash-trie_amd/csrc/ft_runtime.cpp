@@ -123,6 +123,10 @@ struct ft_ctx {
   uint32_t wgs_req = 4096;    // workgroups per request (clamped to residency:
                               // a lone request gets every CU)
   uint32_t share_min = 4096;  // work items from which a step is shared
+  // a streamed search publishes each request's first head_rows rows before
+  // it packs the rest of any (0: whole requests); helper 1 of the request
+  // copies the rest to the device while the leader searches
+  uint32_t head_rows = 3;
   // test knob: helpers never claim their slices, so the leader takes every
   // one over after its grace period
   uint32_t no_claims = 0;
@@ -703,6 +707,10 @@ int ft_create(const void* image, size_t image_bytes, int device,
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->scan_mult = (uint32_t)v;
   }
+  if (const char* s = std::getenv("FT_HEAD_ROWS")) {
+    const long v = std::strtol(s, nullptr, 10);
+    if (v >= 0 && v < 1000000) c->head_rows = (uint32_t)v;
+  }
   *out = c;
   return FT_OK;
 }
@@ -943,26 +951,44 @@ static const ScanRowFn g_scan_row =
 // caller's rows are staged only when some row is out of order (else rk_off
 // is 0 and the index is the position), and in_bytes ends the block there.
 // Fails on NaN / +inf logps, duplicate token ids in a row and non-finite
-// length-norm factors.  `tmp` holds K pairs.
-static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
-                        std::pair<uint32_t, uint32_t>* tmp, std::string* err) {
-  auto who = [r]() { return "request " + std::to_string(r) + ": "; };
-  const uint32_t T = d.T, K = d.K;
+// length-norm factors.  `tmp` holds K pairs.  In three parts, so that a
+// streamed search can publish a request's first rows before the rest:
+// pack_head (length-norm table, beam widths), pack_rows (rows t0 .. t1 - 1
+// and their key bounds, in order), pack_end (rk_off, in_bytes).
+struct PackState {
+  double s_lo = 0.0, s_hi = 0.0;  // bounds of the parent scores at the next row
+  uint32_t rk_planned = 0;        // where the row indices go when a row needs them
+  bool rk_used = false;
+};
+
+static int pack_head(const ft_request& q, size_t r, DevReq& d, uint8_t* base, PackState& ps,
+                     std::string* err) {
+  const uint32_t T = d.T;
   // length-norm table, exactly Agent::logp_norm's factor (agent.h:69-72)
   double* lnf = (double*)base;
   // (depth 0 is the root alone, whose norm is never compared)
   for (uint32_t dd = 0; dd <= T; ++dd) {
     lnf[dd] = std::pow(6.0 / (5.0 + (double)dd), q.length_norm);
     if (dd > 0 && !std::isfinite(lnf[dd]))
-      return *err = who() + "length_norm gives a non-finite factor", FT_E_INPUT;
+      return *err = "request " + std::to_string(r) + ": length_norm gives a non-finite factor",
+             FT_E_INPUT;
   }
   std::memcpy(base + d.beams_off, q.beams, 4ull * T);
+  ps = PackState();
+  // d.rk_off holds the planned offset of the indices until a row needs them
+  ps.rk_planned = d.rk_off;
+  return FT_OK;
+}
+
+static int pack_rows(const ft_request& q, size_t r, const DevReq& d, uint8_t* base, uint32_t t0,
+                     uint32_t t1, std::pair<uint32_t, uint32_t>* tmp, PackState& ps,
+                     std::string* err) {
+  auto who = [r]() { return "request " + std::to_string(r) + ": "; };
+  const uint32_t K = d.K;
+  const double* lnf = (const double*)base;
   uint32_t* rid_s = (uint32_t*)(base + d.rid_off);
   float* rlp_s = (float*)(base + d.rlp_off);
-  // d.rk_off holds the planned offset of the indices until a row needs them
-  const uint32_t rk_planned = d.rk_off;
-  uint16_t* rk_s = (uint16_t*)(base + rk_planned);
-  bool rk_used = false;
+  uint16_t* rk_s = (uint16_t*)(base + ps.rk_planned);
   uint64_t* kb = (uint64_t*)(base + d.kb_off);
   // Per step, bounds of the keys pushed into `next`: a push's score is a
   // parent score plus a logp that passes the token threshold, and itself
@@ -971,8 +997,7 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
   // by the length factor are monotone, so the bounds hold exactly for the
   // device's arithmetic (which this repeats).  A row with no logp above
   // the threshold contributes 0 to both bounds (it pushes nothing).
-  double s_lo = 0.0, s_hi = 0.0;  // parent scores at step t
-  for (uint32_t t = 0; t < T; ++t) {
+  for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t* rid = q.topk_id_rows ? q.topk_id_rows[t] : q.topk_id + (uint64_t)t * K;
     const float* rlp = q.topk_logp_rows ? q.topk_logp_rows[t] : q.topk_logp + (uint64_t)t * K;
     if (!rid || !rlp) return *err = who() + "null topk row", FT_E_ARG;
@@ -984,12 +1009,12 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
     const RowScan sc = g_scan_row(rid, rlp, K, q.token_logp_threshold, oid, olp);
     if (sc.bad) return *err = who() + "topk_logp holds NaN or +inf", FT_E_INPUT;
     if (sc.sorted) {
-      if (rk_used)
+      if (ps.rk_used)
         for (uint32_t k = 0; k < K; ++k) ok[k] = (uint16_t)k;
     } else {
-      if (!rk_used) {  // the rows before this one, in order: index = position
+      if (!ps.rk_used) {  // the rows before this one, in order: index = position
         for (uint64_t i = 0; i < (uint64_t)t * K; ++i) rk_s[i] = (uint16_t)(i % K);
-        rk_used = true;
+        ps.rk_used = true;
       }
       for (uint32_t k = 0; k < K; ++k) tmp[k] = {rid[k], k};
       std::sort(tmp, tmp + K);
@@ -1005,15 +1030,28 @@ static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
     }
     const bool any = sc.hi >= sc.lo;
     const double x_lo = any ? (double)sc.lo : 0.0, x_hi = any ? (double)sc.hi : 0.0;
-    const double lo = std::max(q.sent_logp_threshold, s_lo + x_lo);
-    const double hi = s_hi + x_hi;
+    const double lo = std::max(q.sent_logp_threshold, ps.s_lo + x_lo);
+    const double hi = ps.s_hi + x_hi;
     kb[2 * t] = host_norm_key(lo * lnf[t + 1]);
     kb[2 * t + 1] = host_norm_key(hi * lnf[t + 1]);
-    s_lo = lo;
-    s_hi = hi;
+    ps.s_lo = lo;
+    ps.s_hi = hi;
   }
-  d.rk_off = rk_used ? rk_planned : 0u;
-  d.in_bytes = rk_used ? (uint32_t)align_up(rk_planned + 2ull * T * K, 16) : rk_planned;
+  return FT_OK;
+}
+
+static void pack_end(DevReq& d, const PackState& ps) {
+  d.rk_off = ps.rk_used ? ps.rk_planned : 0u;
+  d.in_bytes = ps.rk_used ? (uint32_t)align_up(ps.rk_planned + 2ull * d.T * d.K, 16)
+                          : ps.rk_planned;
+}
+
+static int pack_request(const ft_request& q, size_t r, DevReq& d, uint8_t* base,
+                        std::pair<uint32_t, uint32_t>* tmp, std::string* err) {
+  PackState ps;
+  if (int rc = pack_head(q, r, d, base, ps, err)) return rc;
+  if (int rc = pack_rows(q, r, d, base, 0, d.T, tmp, ps, err)) return rc;
+  pack_end(d, ps);
   return FT_OK;
 }
 
@@ -1236,6 +1274,7 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.wdir_log2 = c->wdir_log2;
   a.wide_min = c->wide_min;
   a.no_claims = c->no_claims;
+  a.head_rows = 0;
   a.louds_words = c->d_louds_words;
   a.louds_z = c->d_louds_z;
   a.louds_s = c->d_louds_s;
@@ -1433,21 +1472,63 @@ struct PackJob {
   unsigned long long* ready;
   unsigned long long tag;
   size_t batch;
+  // rows a request's first ready word carries (0: all of them)
+  uint32_t head_rows = 0;
   std::vector<int> rc;
   std::vector<std::string> msg;
 };
 
-// Packs the requests of `j` in order, writing each one's ready word as soon
-// as it is packed (a skipped request's workgroups return at once and need
-// none); `tmp` holds max_topk pairs.
+// Packs the requests of `j` and writes their ready words (a skipped
+// request's workgroups return at once and need none); `tmp` holds max_topk
+// pairs.  First, request by request, the length-norm table, beam widths and
+// the rows before its split (stream_split), then a kReadyPart word; then, again request by
+// request, the other rows, with a kReadyPart word after each, and the
+// kReadyOk word.  So every request of a batch can start after a short
+// first pass, and its leader finds the other rows when it needs them.  A
+// request that fails to pack is withdrawn at once.
 void pack_stream(PackJob& j, std::pair<uint32_t, uint32_t>* tmp) {
-  for (size_t r = 0; r < j.batch; ++r) {
-    if (j.staged[r].skip) continue;
-    const int rc = pack_request(j.reqs[r], r, j.D[r], j.H + j.D[r].in_off, tmp, &j.msg[r]);
-    j.rc[r] = rc;
+  std::vector<PackState> ps(j.batch);
+  auto publish = [&](size_t r, unsigned long long state) {
     // the block's stores (non-temporal ones included) before the word
     _mm_sfence();
-    __atomic_store_n(&j.ready[r], j.tag | (rc ? kReadyWithdrawn : kReadyOk), __ATOMIC_RELEASE);
+    __atomic_store_n(&j.ready[r], j.tag | state, __ATOMIC_RELEASE);
+  };
+  auto rows_word = [&](size_t r, uint32_t rows) {
+    return ((unsigned long long)rows << kReadyRowsShift) | kReadyPart |
+           (ps[r].rk_used ? kReadyRk : 0u);
+  };
+  auto withdraw = [&](size_t r, int rc) {
+    j.rc[r] = rc;
+    publish(r, kReadyWithdrawn);
+  };
+  auto finish = [&](size_t r) {
+    pack_end(j.D[r], ps[r]);
+    publish(r, ((unsigned long long)j.D[r].T << kReadyRowsShift) | kReadyOk |
+                   (ps[r].rk_used ? kReadyRk : 0u));
+  };
+  for (size_t r = 0; r < j.batch; ++r) {
+    if (j.staged[r].skip) continue;
+    DevReq& d = j.D[r];
+    uint8_t* base = j.H + d.in_off;
+    const uint32_t h = stream_split(j.head_rows, d.T, d.K);
+    int rc = pack_head(j.reqs[r], r, d, base, ps[r], &j.msg[r]);
+    if (!rc) rc = pack_rows(j.reqs[r], r, d, base, 0, h, tmp, ps[r], &j.msg[r]);
+    if (rc) withdraw(r, rc);
+    else if (h == d.T) finish(r);
+    else publish(r, rows_word(r, h));
+  }
+  for (size_t r = 0; r < j.batch; ++r) {
+    DevReq& d = j.D[r];
+    const uint32_t h = stream_split(j.head_rows, d.T, d.K);
+    if (j.staged[r].skip || j.rc[r] || h >= d.T) continue;
+    uint8_t* base = j.H + d.in_off;
+    int rc = FT_OK;
+    for (uint32_t t = h; t < d.T && !rc; ++t) {
+      rc = pack_rows(j.reqs[r], r, d, base, t, t + 1, tmp, ps[r], &j.msg[r]);
+      if (!rc && t + 1 < d.T) publish(r, rows_word(r, t + 1));
+    }
+    if (rc) withdraw(r, rc);
+    else finish(r);
   }
 }
 }  // namespace
@@ -1526,6 +1607,7 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   a.ready = c->m_ready;
   a.out_host = c->m_out;
   a.stage_bytes = used;
+  a.head_rows = c->head_rows;
   // the result headers start unpublished
   for (size_t r = 0; r < batch; ++r)
     __atomic_store_n(&((OutHeader*)(c->h_out + c->out_stride * r))->status, 0u, __ATOMIC_RELAXED);
@@ -1538,6 +1620,7 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   job.ready = c->h_ready;
   job.tag = (unsigned long long)a.epoch << 32;
   job.batch = batch;
+  job.head_rows = a.head_rows;
   job.rc.assign(batch, FT_OK);
   job.msg.resize(batch);
   pack_stream(job, c->sort_tmp.data());

@@ -28,9 +28,31 @@ enum : uint32_t {
   kStatusDone = 0x80000000u,
 };
 
-// Streamed search: the ready word of a request, (launch epoch << 32) | state,
-// written by the host once the request's block is packed (or withdrawn).
-enum : uint32_t { kReadyOk = 1u, kReadyWithdrawn = 2u };
+// Streamed search: the ready word of a request, (launch epoch << 32) |
+// (rows << kReadyRowsShift) | state, written by the host as the request's
+// block is packed: kReadyPart once its length-norm table, beam widths and
+// first `rows` rows (with their key bounds) are, kReadyOk once all of it
+// is (rows = T), or kReadyWithdrawn when it failed to pack.  kReadyRk is
+// added once a row has come out of order: from then on the proposal indices
+// of every packed row are in the block, at the DevReq's planned rk_off.
+enum : uint32_t { kReadyOk = 1u, kReadyWithdrawn = 2u, kReadyPart = 4u, kReadyRk = 8u };
+// The split of a streamed request between its first ready word and the
+// rest: the first row h >= head_rows (head_rows > 0) with h * K a multiple of
+// 8, so that every row array (u32 tokens, f32 logps, u16 indices) splits on
+// a 16-byte boundary; T (no split) when there is none before T.  The host
+// and the kernel compute it alike.
+__host__ __device__ inline uint32_t stream_split(uint32_t head_rows, uint32_t T, uint32_t K) {
+  if (head_rows == 0 || head_rows >= T) return T;
+  uint32_t h = head_rows;
+  while (h < T && ((uint64_t)h * K) % 8u != 0u) ++h;
+  return h;
+}
+// States of the copy word of a streamed search (Ctl::copy): claimed, done
+// (with the row indices when kCopyRk is added too), or failed (the request
+// was withdrawn or its rows never came).
+enum : uint32_t { kCopyClaimed = 1u, kCopyDone = 2u, kCopyRk = 4u, kCopyFailed = 8u };
+constexpr uint32_t kReadyRowsShift = 8;
+constexpr uint32_t kReadyStateMask = 0xFFu;
 // How long a leader waits for its ready word (wall-clock ticks of 10 ns).
 constexpr unsigned long long kReadyTicks = 100000000ull;
 
@@ -192,7 +214,10 @@ struct Ctl {
   // counters of the step (atomics)
   uint32_t n_next, n_sel;
   unsigned long long children, probes;
-  uint32_t pad3[18];
+  // streamed search: the copy of the rows after the first ready word's
+  // (launch epoch << 32) | kCopy* state, claimed by helper 1 or the leader
+  unsigned long long copy;
+  uint32_t pad3[16];
 };
 static_assert(sizeof(Ctl) == 384, "Ctl layout");
 
@@ -231,7 +256,9 @@ struct KArgs {
   // helpers never claim their slices (a test of the leader's take-over of
   // unclaimed slices; never set otherwise)
   uint32_t no_claims;
-  uint32_t pad1;
+  // streamed search: rows of a request its first ready word carries (0:
+  // all of them); helper 1 copies the rest once the host has packed them
+  uint32_t head_rows;
   // Child ranges from the LOUDS rank/select directory instead of the node
   // records' child_begin (null: records), see LoudsDir.
   const uint64_t* louds_words;  // the LOUDS bits, 64 a word

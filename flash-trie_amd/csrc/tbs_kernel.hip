@@ -1241,71 +1241,270 @@ __device__ __forceinline__ uint32_t caller_index(const uint16_t* rk, uint32_t t,
   return rk ? (uint32_t)rk[(uint64_t)t * K + p] : p;
 }
 
-// Streamed search, the leader's start: thread 0 waits (bounded) for the
-// request's ready word in host memory -- a system-scope acquire, so that
-// what the host packed before it is what the reads below see -- and the
-// workgroup then copies the packed block from mapped host memory to the
-// device stage, with device-coherent stores: helpers read its rows from
-// there in shared steps, after the leader's first post (which follows the
-// wait for these stores).  Returns the request's rk_off as packed (the rest
-// of its header was final at the launch), or kStageFailed when the host
-// withdrew the request or the word never came, after releasing the helpers
-// and reporting the status in out_host.
-constexpr uint32_t kStageFailed = 0xFFFFFFFFu;
-__device__ __forceinline__ uint32_t stage_in(const KArgs& a, uint32_t req, uint8_t* ws,
-                                             Smem& sm) {
-  const uint32_t tid = threadIdx.x;
-  const unsigned long long tag = (unsigned long long)a.epoch << 32;
-  if (tid == 0) {
+// Streamed search: how much of its block the leader has copied from mapped
+// host memory into the device stage (values every thread holds alike).
+struct StageState {
+  uint32_t rows;     // rows, with their key bounds, in the stage
+  uint32_t rk_rows;  // rows whose proposal indices are in the stage
+  uint32_t split;    // rows of the first ready word (stream_split)
+  bool rk;           // some row came out of order: its indices are read
+  bool done;         // the whole block is in
+  bool own;          // the leader claimed the copy of the rows after `split`
+};
+
+// Thread 0 waits (bounded) for request req's ready word to carry this
+// launch's epoch and a final state or at least `need` rows -- a system-scope
+// acquire, so that what the host packed before the word is what the reads
+// after it see.  Returns the word to every thread, or 0 when it never came.
+__device__ __forceinline__ unsigned long long wait_ready(const KArgs& a, uint32_t req,
+                                                         uint32_t need, Smem& sm) {
+  if (threadIdx.x == 0) {
     const unsigned long long t0 = wall_clock64();
     unsigned long long v = 0;
     for (;;) {
       v = __hip_atomic_load(a.ready + req, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-      if ((v >> 32) == a.epoch || wall_clock64() - t0 > kReadyTicks) break;
+      if ((v >> 32) == a.epoch &&
+          (((uint32_t)v & (kReadyOk | kReadyWithdrawn)) ||
+           ((uint32_t)v >> kReadyRowsShift) >= need))
+        break;
+      if (wall_clock64() - t0 > kReadyTicks) {
+        v = 0;
+        break;
+      }
       __builtin_amdgcn_s_sleep(2);
     }
     sm.bcast = v;
   }
   __syncthreads();
-  const unsigned long long v = sm.bcast;
-  const DevReq d = a.reqs[req];
-  const bool fits = d.in_off + d.in_bytes <= a.stage_bytes && (d.in_bytes & 15u) == 0;
-  if (v != (tag | kReadyOk) || !fits) {
-    if (tid == 0) {
-      st_dev(&((Ctl*)(ws + a.lay.ctl))->go, tag | kGoExit);
-      OutHeader* oh = (OutHeader*)(a.out_host + (uint64_t)req * a.out_stride);
-      oh->count = 0;
-      const uint32_t st = v == (tag | kReadyWithdrawn) ? kStatusWithdrawn
-                          : v == (tag | kReadyOk)      ? kStatusStage
-                                                       : kStatusNotReady;
-      __hip_atomic_store(&oh->status, st | kStatusDone, __ATOMIC_RELEASE,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    return kStageFailed;
+  return sm.bcast;
+}
+
+// Copies the byte ranges [b[i], e[i]) of the request's block (each rounded
+// out to 16 bytes; none when e[i] <= b[i]) from mapped host memory to the
+// device stage, with device-coherent stores: helpers read its rows there.
+// Every thread; the loads of a round are all in flight together.  Ends
+// synchronised, with the stores complete.  Callers give ranges whose
+// rounding takes in only bytes the host has packed for good.
+constexpr uint32_t kNoWord = 0xFFFFFFFFu;
+template <uint32_t kU>
+__device__ __forceinline__ void stage_copy(const KArgs& a, uint64_t in_off, const uint32_t (&b)[4],
+                                           const uint32_t (&e)[4]) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t s16[4], n16[4], total = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = b[r] & ~15u, hi = (e[r] + 15u) & ~15u;
+    s16[r] = lo / 16u;
+    n16[r] = e[r] > b[r] ? (hi - lo) / 16u : 0u;
+    total += n16[r];
   }
-  const uint4* src = (const uint4*)(a.stage_src + d.in_off);
-  unsigned long long* dst = (unsigned long long*)(const_cast<uint8_t*>(a.stage) + d.in_off);
-  const uint32_t n16 = d.in_bytes / 16u;
-  constexpr uint32_t kU = 8;  // loads in flight per thread
-  for (uint32_t i0 = 0; i0 < n16; i0 += kBlock * kU) {
+  const uint4* src = (const uint4*)(a.stage_src + in_off);
+  unsigned long long* dst = (unsigned long long*)(const_cast<uint8_t*>(a.stage) + in_off);
+  for (uint32_t i0 = 0; i0 < total; i0 += kBlock * kU) {
     uint4 w[kU];
+    uint32_t at[kU];
 #pragma unroll
     for (uint32_t u = 0; u < kU; ++u) {
-      const uint32_t i = i0 + u * kBlock + tid;
-      if (i < n16) w[u] = src[i];
+      uint32_t i = i0 + u * kBlock + tid;
+      at[u] = kNoWord;
+      if (i < total) {
+        uint32_t x;
+        if (i < n16[0]) {
+          x = s16[0] + i;
+        } else if ((i -= n16[0]) < n16[1]) {
+          x = s16[1] + i;
+        } else if ((i -= n16[1]) < n16[2]) {
+          x = s16[2] + i;
+        } else {
+          x = s16[3] + (i - n16[2]);
+        }
+        at[u] = x;
+        w[u] = src[x];
+      }
     }
 #pragma unroll
     for (uint32_t u = 0; u < kU; ++u) {
-      const uint32_t i = i0 + u * kBlock + tid;
-      if (i < n16) {
-        st_dev(dst + 2 * i, pack2(w[u].x, w[u].y));
-        st_dev(dst + 2 * i + 1, pack2(w[u].z, w[u].w));
+      if (at[u] != kNoWord) {
+        st_dev(dst + 2ull * at[u], pack2(w[u].x, w[u].y));
+        st_dev(dst + 2ull * at[u] + 1, pack2(w[u].z, w[u].w));
       }
     }
   }
   wait_stores();
   __syncthreads();
-  return d.rk_off;
+}
+
+// The planned block fits the stage and its arrays fit the block.
+__device__ __forceinline__ bool block_fits(const KArgs& a, const DevReq& d) {
+  const uint64_t T = d.T, K = d.K;
+  return d.in_off + d.in_bytes <= a.stage_bytes && (d.in_bytes & 15u) == 0 &&
+         d.beams_off + 4 * T <= d.in_bytes && d.kb_off + 16 * T <= d.in_bytes &&
+         d.rid_off + 4 * T * K <= d.in_bytes && d.rlp_off + 4 * T * K <= d.in_bytes &&
+         d.rk_off + 2 * T * K <= d.in_bytes;
+}
+
+// Rows [h0, h1) of the request's block with their key bounds (with `head`,
+// everything before the bounds too: the length-norm table and beam widths)
+// and, when the ready word `v` carries kReadyRk, the proposal indices of
+// rows [ss.rk_rows, h1); then records them in ss.  Every thread; ends
+// synchronised.
+template <uint32_t kU>
+__device__ __forceinline__ void stage_rows(const KArgs& a, const DevReq& d, bool head,
+                                           uint32_t h0, uint32_t h1, unsigned long long v,
+                                           StageState& ss) {
+  const uint32_t rb = 4u * d.K;  // bytes of a row of tokens (and of logps)
+  const bool rk = ((uint32_t)v & kReadyRk) != 0;
+  const uint32_t b[4] = {head ? 0u : d.kb_off + 16u * h0, d.rid_off + h0 * rb,
+                         d.rlp_off + h0 * rb, d.rk_off + ss.rk_rows * 2u * d.K};
+  const uint32_t e[4] = {d.kb_off + 16u * h1, d.rid_off + h1 * rb, d.rlp_off + h1 * rb,
+                         rk ? d.rk_off + h1 * 2u * d.K : 0u};
+  stage_copy<kU>(a, d.in_off, b, e);
+  ss.rows = h1;
+  if (rk) {
+    ss.rk = true;
+    ss.rk_rows = h1;
+  }
+  ss.done = h1 >= d.T;
+}
+
+// Streamed search, the leader's start: waits for the request's first ready
+// word and copies its length-norm table, beam widths and first rows (all of
+// them when the word is final, else those before its split) to the device
+// stage; helpers read rows there in shared steps, after the leader's first
+// post (which follows the wait for these stores).  `d` is the request's
+// header as planned at the launch: its offsets are final then (rk_off is
+// where the indices go when some row needs them).  False when the host
+// withdrew the request, the word never came or the planned block does not
+// fit the stage -- after releasing the helpers and reporting the status in
+// out_host.
+__device__ __forceinline__ bool stage_in(const KArgs& a, uint32_t req, const DevReq& d,
+                                         uint8_t* ws, StageState& ss, Smem& sm) {
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  const uint32_t split = stream_split(a.head_rows, d.T, d.K);
+  const unsigned long long v = wait_ready(a, req, split, sm);
+  const uint32_t rows = (uint32_t)v >> kReadyRowsShift;
+  const bool final = ((uint32_t)v & kReadyOk) != 0;
+  const bool ok = (v >> 32) == a.epoch && !((uint32_t)v & kReadyWithdrawn) &&
+                  (final ? rows == d.T : ((uint32_t)v & kReadyPart) && rows >= split &&
+                                             rows < d.T);
+  if (!ok || !block_fits(a, d)) {
+    if (threadIdx.x == 0) {
+      st_dev(&((Ctl*)(ws + a.lay.ctl))->go, tag | kGoExit);
+      OutHeader* oh = (OutHeader*)(a.out_host + (uint64_t)req * a.out_stride);
+      oh->count = 0;
+      const uint32_t st = ((v >> 32) == a.epoch && ((uint32_t)v & kReadyWithdrawn))
+                              ? kStatusWithdrawn
+                          : ok ? kStatusStage
+                               : kStatusNotReady;
+      __hip_atomic_store(&oh->status, st | kStatusDone, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    return false;
+  }
+  ss = StageState{0u, 0u, split, false, false, false};
+  stage_rows<8>(a, d, true, 0u, final ? d.T : split, v, ss);
+  return true;
+}
+
+// Streamed search, helper 1 at its start: the copy of the request's rows
+// after the split (with their bounds, and all of its proposal indices when
+// some row came out of order) -- claimed here unless the leader claimed it
+// first -- once the host has packed the whole request, while the leader
+// searches the first rows.  The copy word then says done or failed.
+__device__ __forceinline__ void helper_copy(const KArgs& a, uint32_t req, const DevReq& d,
+                                            uint8_t* ws, Smem& sm) {
+  const uint32_t split = stream_split(a.head_rows, d.T, d.K);
+  if (split >= d.T) return;
+  Ctl* ctl = (Ctl*)(ws + a.lay.ctl);
+  const unsigned long long tag = (unsigned long long)a.epoch << 32;
+  if (threadIdx.x == 0)
+    sm.lead_flag = atomicMax(&ctl->copy, tag | kCopyClaimed) < (tag | kCopyClaimed) ? 1u : 0u;
+  __syncthreads();
+  const bool mine = sm.lead_flag != 0;
+  __syncthreads();
+  if (!mine) return;
+  const unsigned long long v = wait_ready(a, req, d.T, sm);
+  const bool ok = (v >> 32) == a.epoch && ((uint32_t)v & kReadyOk) &&
+                  ((uint32_t)v >> kReadyRowsShift) == d.T && block_fits(a, d);
+  const bool rk = ((uint32_t)v & kReadyRk) != 0;
+  if (ok) {
+    const uint32_t rb = 4u * d.K;
+    const uint32_t b[4] = {d.kb_off + 16u * split, d.rid_off + split * rb, d.rlp_off + split * rb,
+                           d.rk_off};
+    const uint32_t e[4] = {d.kb_off + 16u * d.T, d.rid_off + d.T * rb, d.rlp_off + d.T * rb,
+                           rk ? d.rk_off + 2u * d.T * d.K : 0u};
+    stage_copy<8>(a, d.in_off, b, e);
+  }
+  if (threadIdx.x == 0)
+    st_dev(&ctl->copy, tag | (ok ? (kCopyDone | (rk ? kCopyRk : 0u)) : kCopyFailed));
+  __syncthreads();
+}
+
+// Streamed search: makes rows up to u (< T) of the request available in the
+// device stage, a no-op once they are.  The rows after the split come from
+// helper 1's copy, waited for when it has claimed it (it is running then),
+// else from the leader, which claims the copy and takes the rows as the host
+// packs them.  False when the request was withdrawn or the rows never came
+// (the status is in sm.status then).  Every thread; ends synchronised.
+__device__ __forceinline__ bool ensure_rows(const KArgs& a, uint32_t req, const DevReq& d,
+                                            uint8_t* ws, uint32_t u, StageState& ss, Smem& sm) {
+  if (ss.done || u < ss.rows) return true;
+  uint32_t fail = 0;
+  if (!ss.own) {
+    Ctl* ctl = (Ctl*)(ws + a.lay.ctl);
+    const unsigned long long tag = (unsigned long long)a.epoch << 32;
+    if (threadIdx.x == 0) {
+      unsigned long long c = atomicMax(&ctl->copy, tag | kCopyClaimed);
+      uint32_t st = kCopyClaimed;  // claimed now by the leader
+      if (c >= (tag | kCopyClaimed)) {
+        // helper 1 has it: wait (bounded) for its end
+        const unsigned long long t0 = wall_clock64();
+        while ((uint32_t)c == kCopyClaimed && wall_clock64() - t0 <= kReadyTicks) {
+          __builtin_amdgcn_s_sleep(2);
+          c = ld_relaxed(&ctl->copy);
+        }
+        st = (uint32_t)c == kCopyClaimed ? kCopyFailed : (uint32_t)c;
+      } else {
+        st = 0u;  // the leader's own
+      }
+      sm.lead_flag = st;
+    }
+    __syncthreads();
+    const uint32_t st = sm.lead_flag;
+    __syncthreads();
+    if (st & kCopyDone) {
+      // helper 1's stores were complete before its word: drop stale lines
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      ss.rows = d.T;
+      ss.done = true;
+      if (st & kCopyRk) {
+        ss.rk = true;
+        ss.rk_rows = d.T;
+      }
+      return true;
+    }
+    if (st & kCopyFailed) fail = kStatusNotReady;
+    ss.own = true;
+  }
+  unsigned long long v = 0;
+  if (!fail) {
+    v = wait_ready(a, req, u + 1u, sm);
+    const uint32_t rows = (uint32_t)v >> kReadyRowsShift;
+    if ((v >> 32) != a.epoch || ((uint32_t)v & kReadyWithdrawn) || rows <= u || rows > d.T)
+      fail = ((v >> 32) == a.epoch && ((uint32_t)v & kReadyWithdrawn)) ? kStatusWithdrawn
+                                                                       : kStatusNotReady;
+  }
+  if (fail) {
+    if (threadIdx.x == 0) sm.status |= fail;
+    __syncthreads();
+    return false;
+  }
+  stage_rows<4>(a, d, false, ss.rows, (uint32_t)v >> kReadyRowsShift, v, ss);
+  // The leader reads rows and bounds with ordinary loads, and a row ends
+  // inside a cache line: its L1 may hold the start of a row this copy just
+  // wrote, read before with the end of the row in front.  Drop such lines.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return true;
 }
 
 // A helper workgroup: waits for shared steps of its request and expands its
@@ -1321,6 +1520,9 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
   const double* lnf = (const double*)in;
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
   const float* rlp = (const float*)(in + d.rlp_off);
+  if constexpr (kStreamed) {
+    if (g == 1) helper_copy(a, blockIdx.x % a.batch, d, ws, sm);
+  }
   row_hash_clear(sm);  // (visible after the first barrier below)
   for (;;) {
     if (tid == 0) {
@@ -1800,14 +2002,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   }
 
   // ---- the leader ----------------------------------------------------------
-  uint32_t rk_off = d.rk_off;
   // the per-step profile goes to `out` during the search; the results (and
   // a copy of the profile) to out_host in a streamed search, else to `out`
   uint8_t* ob = a.out + (uint64_t)req * a.out_stride;
+  // a streamed request's rows come to the device stage as the host packs
+  // them (stage_in, ensure_rows); the staged search has them all
+  StageState ss{d.T, d.T, d.T, d.rk_off != 0u, true, false};
   if constexpr (kStreamed) {
-    rk_off = stage_in(a, req, ws, sm);
-    if (rk_off == kStageFailed) return;
-    rk_off = uni(rk_off);
+    if (!stage_in(a, req, d, ws, ss, sm)) return;
     if (tid == 0) sm.res_host = (unsigned long long)(a.out_host + (uint64_t)req * a.out_stride);
   }
   const uint8_t* in = a.stage + uni(d.in_off);
@@ -1815,7 +2017,17 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   const uint32_t* beams = (const uint32_t*)(in + d.beams_off);
   const uint32_t* rid = (const uint32_t*)(in + d.rid_off);
   const float* rlp = (const float*)(in + d.rlp_off);
-  const uint16_t* rk = rk_off ? (const uint16_t*)(in + rk_off) : nullptr;
+  // the proposals' indices in the caller's rows, when some row came out of
+  // order (else index = position)
+  const uint16_t* rk = ss.rk ? (const uint16_t*)(in + d.rk_off) : nullptr;
+  // (streamed) rows up to u in the device stage, or false with sm.status set
+  auto rows_upto = [&](uint32_t u) {
+    if constexpr (kStreamed) {
+      if (!ensure_rows(a, req, d, ws, u, ss, sm)) return false;
+      rk = ss.rk ? (const uint16_t*)(in + d.rk_off) : nullptr;
+    }
+    return true;
+  };
   const uint32_t T = d.T, K = d.K, F = d.F;
   const bool early = (d.flags & kReqEarlyExit) != 0;
 
@@ -1905,6 +2117,10 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         bool first = true, finished = false;
         for (;;) {
           const uint32_t nr = min(R, T - t);
+          if (!rows_upto(t + nr - 1u)) {
+            finished = true;
+            break;
+          }
           tail_fill(a, rid, rlp, beams, t, nr, K, Kp, n_cur, sm);
           __syncthreads();
           if (tid < 64u) tiny_steps(a, d, t, nr, Kp, first, n_cur, nS, hist_used, lane, lnf,
@@ -1931,6 +2147,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         if (n_cur == 0 || (early && nS >= F)) break;
       }
     }
+    // this step's row, and the next one, which the step reads ahead
+    if (!rows_upto(min(t + 1u, T - 1u))) break;
     const unsigned long long t0 = wall_clock64();
     const uint32_t ncur0 = n_cur;
     if (row_pf) {
@@ -2089,6 +2307,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // visible)
     const bool hashed = K <= kRowHashMaxK && W >= kRowHashMinWork;
     if (hashed) hash_row(K, sm);
+    // (streamed) helper 1 copying the request's later rows claims no slice
+    // meanwhile: its slice is taken over at once rather than after the
+    // grace period (thread 0 stands for slot 1 below)
+    bool copying1 = false;
+    if constexpr (kStreamed) {
+      if (shared && tid == 0 && !ss.done && !ss.own && ss.split < T)
+        copying1 = ld_relaxed(&ctl->copy) == (tag | kCopyClaimed);
+    }
     expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared,
                  hashed, sm);
     if (shared) {
@@ -2103,7 +2329,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       const uint32_t nh = a.wgs - 1;  // helper slots 1 .. nh (nh < kBlock)
       bool pending_any = true;
       for (;;) {
-        const int pending = __syncthreads_count(tid < nh && ld_relaxed(&claims[tid + 1]) != mygo);
+        const int pending = __syncthreads_count(tid < nh && !copying1 &&
+                                                ld_relaxed(&claims[tid + 1]) != mygo);
         if (pending == 0) {
           pending_any = false;
           break;

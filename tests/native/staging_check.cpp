@@ -151,9 +151,12 @@ int main() {
     }
   }
   // The streamed search's packing: plan_batch lays the batch out, then
-  // pack_stream packs the requests and writes their ready words.  The blocks
-  // must equal pack_batch's; a request with a NaN is withdrawn (and only it
-  // -- the others stay ready), where pack_batch fails.
+  // pack_stream packs the requests and writes their ready words -- whole
+  // requests, or the first 1 or 3 rows of every request before the rest.
+  // The blocks must equal pack_batch's; each final word holds the row count
+  // and whether the row indices are staged; a request with a NaN is
+  // withdrawn (and only it -- the others stay ready), where pack_batch
+  // fails.
   int streamed = 0;
   std::vector<uint8_t> H2(8 << 20);
   std::vector<StagedReq> st2(8);
@@ -213,14 +216,19 @@ int main() {
     job.ready = ready.data();
     job.tag = (unsigned long long)(c + 1) << 32;
     job.batch = n;
+    job.head_rows = c % 3 == 0 ? 0u : c % 3 == 1 ? 1u : 3u;
     job.rc.assign(n, FT_OK);
     job.msg.resize(n);
     pack_stream(job, tmp.data());
     for (uint32_t r = 0; r < n; ++r) {
       const bool bad = r == nan_req;
       CHECK((job.rc[r] != FT_OK) == bad, "stream case %d request %u: rc %d", c, r, job.rc[r]);
-      CHECK(ready[r] == (job.tag | (bad ? kReadyWithdrawn : kReadyOk)),
-            "stream case %d request %u: ready word", c, r);
+      const unsigned long long want =
+          bad ? kReadyWithdrawn
+              : ((unsigned long long)T << kReadyRowsShift) | kReadyOk |
+                    (job.D[r].rk_off ? kReadyRk : 0u);
+      CHECK(ready[r] == (job.tag | want), "stream case %d request %u: ready word %llx", c, r,
+            ready[r]);
     }
     if (nan_req == n) {
       CHECK(rc1 == FT_OK, "stream case %d: pack_batch rc %d", c, rc1);

@@ -161,6 +161,45 @@ def test_unsorted_rows(ft, c1):
         assert_same_results((got[0][0], got[1][0]), want, f"unsorted {r}")
 
 
+def test_streamed_rows_arrive_during_the_search(ft, c1):
+    # Batches of 4: the host publishes every request's first rows before it
+    # packs the rest of any, and a leader copies the later rows -- and, once
+    # a row after those comes out of order, the proposal indices of every
+    # row -- when a step first needs them.  Logps rounded to halves make ties,
+    # so the staged indices decide arrival order.
+    t, o, ids, lp = c1
+    rng = np.random.default_rng(11)
+    for b0 in range(0, 32, 4):
+        I, L, want = [], [], []
+        early = (b0 // 4) % 2 == 1
+        for r in range(b0, b0 + 4):
+            i2 = ids[r].copy()
+            l2 = np.round(lp[r] * 2.0) / 2.0
+            if r % 2 == 0:
+                tt = 3 + r % 5
+                perm = rng.permutation(i2.shape[1])
+                i2[tt] = i2[tt][perm]
+                l2[tt] = l2[tt][perm]
+            I.append(i2.tolist())
+            L.append(l2.tolist())
+            want.append(o.tbs([6] * 8, i2, l2, -10.0, -40.0, 5.0, early))
+        got = ft.bs_tbs_gpu(t, 4, [[6] * 8] * 4, I, L, -10.0, -40.0, 5.0, early)
+        for k in range(4):
+            assert_same_results((got[0][k], got[1][k]), want[k], f"streamed rows {b0 + k}")
+    # a NaN in a late row withdraws the batch's call; the next call is sound
+    bad = lp[1].copy()
+    bad[6, 2] = np.nan
+    with pytest.raises(RuntimeError, match="NaN"):
+        ft.bs_tbs_gpu(t, 4, [[6] * 8] * 4, [ids[r].tolist() for r in range(4)],
+                      [lp[0].tolist(), bad.tolist(), lp[2].tolist(), lp[3].tolist()],
+                      -10.0, -40.0, 5.0, False)
+    got = ft.bs_tbs_gpu(t, 4, [[6] * 8] * 4, [ids[r].tolist() for r in range(4)],
+                        [lp[r].tolist() for r in range(4)], -10.0, -40.0, 5.0, False)
+    for k in range(4):
+        want = o.tbs([6] * 8, ids[k], lp[k], -10.0, -40.0, 5.0, False)
+        assert_same_results((got[0][k], got[1][k]), want, f"after withdrawal {k}")
+
+
 def test_mixed_beam_widths(ft, c1):
     t, o, ids, lp = c1
     rng = np.random.default_rng(5)
