@@ -200,6 +200,33 @@ def test_streamed_rows_arrive_during_the_search(ft, c1):
         assert_same_results((got[0][k], got[1][k]), want, f"after withdrawal {k}")
 
 
+@pytest.mark.parametrize("K,T", [(10, 8), (7, 8), (32, 2)])
+def test_streamed_split_rows(ft, c1, K, T):
+    # The split of a streamed request is the first row h >= 3 with h * K a
+    # multiple of 8 (row arrays split on 16 bytes): K = 10 moves it to 4,
+    # K = 7 leaves none before T = 8 (whole requests), T = 2 has none.  Rows
+    # after the split come out of order in half the requests.
+    t, o, ids, lp = c1
+    rng = np.random.default_rng(17 + K + T)
+    for b0 in range(0, 16, 4):
+        I, L, want = [], [], []
+        for r in range(b0, b0 + 4):
+            i2 = ids[r][:T, :K].copy()
+            l2 = lp[r][:T, :K].copy()
+            if r % 2 == 1 and T > 4:
+                tt = 4 + r % (T - 4)
+                perm = rng.permutation(K)
+                i2[tt] = i2[tt][perm]
+                l2[tt] = l2[tt][perm]
+            I.append(i2.tolist())
+            L.append(l2.tolist())
+            want.append(o.tbs([6] * T, i2, l2, -10.0, -40.0, 5.0, False))
+        got = ft.bs_tbs_gpu(t, 4, [[6] * T] * 4, I, L, -10.0, -40.0, 5.0, False)
+        for k in range(4):
+            assert_same_results((got[0][k], got[1][k]), want[k],
+                                f"split K={K} T={T} request {b0 + k}")
+
+
 def test_mixed_beam_widths(ft, c1):
     t, o, ids, lp = c1
     rng = np.random.default_rng(5)
