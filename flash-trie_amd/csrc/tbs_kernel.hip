@@ -989,9 +989,28 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
     bool do_next = false, do_sel = false;
     uint32_t cnode = 0, pj = 0, k = 0, tok = 0;
     double s2 = 0.0;
+    // The chunk's parents, when the table is in LDS: those of its first and
+    // last items (pa, pb) by a 64-ary search of the prefix, two rounds of one
+    // LDS read a lane and a ballot (the prefix is non-decreasing, woff[0] is
+    // 0 and woff[n_par] is W, so each ballot is a run of low lanes); each
+    // lane then searches [pa, pb] alone -- nothing when one parent holds the
+    // whole chunk, as a hashed parent's K items mostly do.
+    uint32_t pa = 0, pb = v.n_par;
+    if (lds_par && !v.one_each) {
+      const uint32_t w0 = c << 6, wl = min(w0 + 63u, W - 1u);
+      const uint32_t st = (v.n_par + 64u) >> 6;  // 64 st > n_par
+      const uint32_t o1 = sm.woff[min(lane * st, v.n_par)];
+      const uint64_t m0 = __ballot(o1 <= w0), m1 = __ballot(o1 <= wl);
+      const uint32_t b0 = (63u - (uint32_t)__clzll((long long)m0)) * st;
+      const uint32_t b1 = (63u - (uint32_t)__clzll((long long)m1)) * st;
+      const uint64_t n0 = __ballot(lane < st && sm.woff[min(b0 + lane, v.n_par)] <= w0);
+      const uint64_t n1 = __ballot(lane < st && sm.woff[min(b1 + lane, v.n_par)] <= wl);
+      pa = b0 + (63u - (uint32_t)__clzll((long long)n0));
+      pb = b1 + (63u - (uint32_t)__clzll((long long)n1)) + 1u;
+    }
     if (w < W) {
       // parent of work item w: the last j with woff[j] <= w
-      uint32_t lo = 0, hi = v.n_par;
+      uint32_t lo = pa, hi = pb;
       if (v.one_each) {
         lo = w;
       } else {
