@@ -756,6 +756,26 @@ struct ParEntry {
 template <bool kLouds>
 __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, uint32_t t,
                                                  uint32_t K, uint32_t* err) {
+  // the node's home group in the table directory is read with its record
+  // (in bounds for any node), not after it: a node with a table then costs
+  // one dependent read, not two.  Buffer loads, so that no branch on
+  // a.wdir sits between the two reads (a directory of 0 bytes when there is
+  // none: its reads return 0 and touch no memory).
+  const uint32_t dmask = a.wdir ? (1u << a.wdir_log2) - 1u : 0u;
+  uint32_t g = a.wdir ? fib_slot(node, a.wdir_log2) : 0u;
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<WideDirGroup*>(a.wdir), 0,
+      a.wdir ? (int)((dmask + 1u) * sizeof(WideDirGroup)) : 0, 0x00020000);
+  const int dof = (int)(g * sizeof(WideDirGroup));
+  uint4 nd, off, lgf;
+  {
+    const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(drs, dof, 0, 0);
+    const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(drs, dof + 16, 0, 0);
+    const auto v2 = __builtin_amdgcn_raw_buffer_load_b128(drs, dof + 32, 0, 0);
+    nd = make_uint4(v0[0], v0[1], v0[2], v0[3]);
+    off = make_uint4(v1[0], v1[1], v1[2], v1[3]);
+    lgf = make_uint4(v2[0], v2[1], v2[2], v2[3]);
+  }
   const ft_node_rec r = a.recs[node];
   uint32_t c0, deg;
   if constexpr (kLouds) {
@@ -784,12 +804,14 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
     e.work = K;
     if (a.wdir && deg >= a.wide_min) {
       // this node has a table: find it in the directory, a 64-B group of
-      // entries per read from the home group on
-      const uint32_t mask = (1u << a.wdir_log2) - 1u;
-      uint32_t g = fib_slot(node, a.wdir_log2);
-      for (uint32_t it = 0; it <= mask; ++it) {
-        const uint4* gp = (const uint4*)&a.wdir[g];
-        const uint4 nd = gp[0], off = gp[1], lgf = gp[2];
+      // entries per read from the home group on (read above)
+      for (uint32_t it = 0; it <= dmask; ++it) {
+        if (it) {
+          const uint4* gp = (const uint4*)&a.wdir[g];
+          nd = gp[0];
+          off = gp[1];
+          lgf = gp[2];
+        }
         const uint32_t nds[4] = {nd.x, nd.y, nd.z, nd.w};
         const uint32_t offs[4] = {off.x, off.y, off.z, off.w};
         const uint32_t lgfs[4] = {lgf.x, lgf.y, lgf.z, lgf.w};
@@ -805,7 +827,7 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
           has_free = has_free || nds[k] == kEmpty;
         }
         if (found || has_free) break;
-        g = (g + 1) & mask;
+        g = (g + 1) & dmask;
       }
     }
   }
