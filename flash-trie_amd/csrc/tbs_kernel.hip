@@ -465,7 +465,9 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
     visit_keys<6>(n, gk, [&](uint32_t, bool ok, uint64_t k) {
       const uint64_t o = k - base;
       const bool act = ok && (o & hi_mask) == prefix;
-      hist_add(act, (uint32_t)((o >> sh) & (nb - 1)), sm.whist);
+      // (the wide bins spread a wave's keys: one LDS add a key, without
+      // hist_add's check for a wave-uniform digit)
+      if (act) atomicAdd(&sm.whist[(uint32_t)((o >> sh) & (nb - 1))], 1u);
     });
     __syncthreads();
     // the bin holding the rem-th key: each thread owns nb / kBlock bins
