@@ -13,6 +13,7 @@
 #include <pybind11/stl.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <chrono>
 #include <cstring>
@@ -28,6 +29,7 @@
 #include "marisa_format.h"
 #include "marisa.h"
 #include "marisa/topk_io.h"
+#include "py_requests.h"
 #include "synth.h"
 #include "trie_impl.h"
 
@@ -73,6 +75,111 @@ struct NpBatch {
 NpBatch& staged_batch() {
   static NpBatch b;
   return b;
+}
+
+// Error of a search, as Trie::tbs_gpu_batched raises it.
+[[noreturn]] void throw_search(int rc) {
+  std::string msg = std::string("tbs_gpu_batched: ") + ft_strerror(rc);
+  const char* d = ft_last_error();
+  if (d && *d) msg += std::string(" (") + d + ")";
+  marisa::ErrorCode code = MARISA_STATE_ERROR;
+  if (rc == FT_E_ARG || rc == FT_E_INPUT) code = MARISA_CODE_ERROR;
+  if (rc == FT_E_LIMIT) code = MARISA_SIZE_ERROR;
+  if (rc == FT_E_NOMEM) code = MARISA_MEMORY_ERROR;
+  throw marisa::Exception(code, msg);
+}
+
+// The GPU search behind bs_tbs_gpu and tbs(use_gpu=True): B requests,
+// either one request's (beams, topk_id, topk_logp) handles or the three
+// batch arguments (`batch`, each indexable by request).  Inputs are read
+// in place (py_requests.h) with the GIL held; the search runs without it;
+// the results become Python lists.  Returns (out_sent, out_logp_norm, ms,
+// phase) like the reference's bs_tbs_gpu: ms is timed from the inputs
+// being in C++ memory to the results being there, as the reference times
+// it (tools/bindings.cpp:90-100), and phase holds per request [expansion,
+// validation, selection, overhead, kernel] device ms.
+py::tuple gpu_search(Trie& trie, size_t B, const py::object* one_beams,
+                     const py::object* one_ids, const py::object* one_lps,
+                     const py::handle* batch, float tok_thr, double sent_thr, double alpha,
+                     bool early) {
+  ft_ctx* c = ctx_of(trie);
+  marisa::TrieImpl* im = trie.impl();
+  // per-thread buffers (the GIL is released during the search, so another
+  // thread may convert its own call meanwhile)
+  struct Buf {
+    std::vector<ftpy::ReqIn> in;
+    std::vector<ft_request> reqs;
+    std::vector<ft_result> res;
+    std::vector<std::vector<double>> norms;
+    std::vector<std::vector<uint32_t>> lens, toks;
+  };
+  static thread_local Buf b;
+  if (b.in.size() < B) {
+    b.in.resize(B);
+    b.norms.resize(B);
+    b.lens.resize(B);
+    b.toks.resize(B);
+  }
+  b.reqs.assign(B, ft_request{});
+  b.res.assign(B, ft_result{});
+  std::vector<py::object> keep;
+  for (size_t i = 0; i < B; ++i) {
+    ftpy::ReqIn& q = b.in[i];
+    if (batch) {
+      const py::object bi = ftpy::batch_item(batch[0], i), ii = ftpy::batch_item(batch[1], i),
+                       li = ftpy::batch_item(batch[2], i);
+      ftpy::read_any(bi, ii, li, q, keep);
+    } else {
+      ftpy::read_any(*one_beams, *one_ids, *one_lps, q, keep);
+    }
+    ft_request& r = b.reqs[i];
+    r.beams = q.beams.data();
+    r.num_beams = (uint32_t)q.beams.size();
+    r.token_logp_threshold = tok_thr;
+    r.sent_logp_threshold = sent_thr;
+    r.length_norm = alpha;
+    r.early_exit = early ? 1 : 0;
+    if (q.F == 0) continue;  // outputs untouched
+    r.num_steps = (uint32_t)q.T;
+    r.topk = (uint32_t)q.K;
+    r.topk_id_rows = q.id_rows.data();
+    r.topk_logp_rows = q.lp_rows.data();
+    // result arrays, grown as needed and never shrunk
+    if (b.norms[i].size() < q.F) b.norms[i].resize(q.F);
+    if (b.lens[i].size() < q.F) b.lens[i].resize(q.F);
+    if (b.toks[i].size() < (size_t)q.F * q.T) b.toks[i].resize((size_t)q.F * q.T);
+    ft_result& o = b.res[i];
+    o.capacity = q.F;
+    o.token_stride = (uint32_t)q.T;
+    o.logp_norm = b.norms[i].data();
+    o.length = b.lens[i].data();
+    o.tokens = b.toks[i].data();
+  }
+  using clk = std::chrono::high_resolution_clock;
+  const auto start = clk::now();
+  int rc;
+  {
+    py::gil_scoped_release nogil;
+    std::lock_guard<std::mutex> lock(im->search_mu);
+    rc = ft_search(c, b.reqs.data(), B, b.res.data(), nullptr);
+  }
+  const auto end = clk::now();
+  if (rc) throw_search(rc);
+  py::list sents(B), norms(B), phase(B);
+  for (size_t i = 0; i < B; ++i) {
+    const ft_result& o = b.res[i];
+    if (b.in[i].F) {
+      auto sl = ftpy::result_lists(o);
+      sents[i] = std::move(sl.first);
+      norms[i] = std::move(sl.second);
+    } else {
+      sents[i] = py::list();
+      norms[i] = py::list();
+    }
+    phase[i] = py::cast(std::vector<double>{o.device_ms[0], 0.0, o.device_ms[1],
+                                            o.device_ms[2], o.device_ms[3]});
+  }
+  return py::make_tuple(sents, norms, marisa::get_msec(start, end), phase);
 }
 
 }  // namespace
@@ -195,23 +302,38 @@ PYBIND11_MODULE(flashtrie, m) {
 
   m.def(
       "tbs",
-      [](Trie& trie, const std::vector<uint32_t>& beams,
-         const std::vector<std::vector<Label>>& topk_id,
-         const std::vector<std::vector<float>>& topk_logp,
-         float token_logp_threshold, double sent_logp_threshold,
-         double length_norm, bool early_exit, bool use_gpu) {
-        std::vector<std::vector<Label>> out_sent;
+      [](Trie& trie, py::object beams, py::object topk_id, py::object topk_logp,
+         float token_logp_threshold, double sent_logp_threshold, double length_norm,
+         bool early_exit, bool use_gpu) -> py::tuple {
+        if (use_gpu) {
+          // one request through the batched path (Trie::tbs_gpu: batch slot 0)
+          py::tuple r = gpu_search(trie, 1, &beams, &topk_id, &topk_logp, nullptr,
+                                   token_logp_threshold, sent_logp_threshold, length_norm,
+                                   early_exit);
+          return py::make_tuple(py::reinterpret_borrow<py::list>(r[0])[0],
+                                py::reinterpret_borrow<py::list>(r[1])[0], r[2]);
+        }
+        // the host search takes the reference's vectors
+        ftpy::ReqIn q;
+        std::vector<py::object> keep;
+        ftpy::read_any(beams, topk_id, topk_logp, q, keep);
+        std::vector<std::vector<Label>> vi(q.T), out_sent;
+        std::vector<std::vector<float>> vl(q.T);
+        for (size_t t = 0; t < q.T; ++t) {
+          vi[t].assign(q.id_rows[t], q.id_rows[t] + q.K);
+          vl[t].assign(q.lp_rows[t], q.lp_rows[t] + q.K);
+        }
         std::vector<double> out_logp_norm;
         auto start = std::chrono::high_resolution_clock::now();
-        TbsInput input{beams, topk_id, topk_logp, out_sent, out_logp_norm,
-                       token_logp_threshold, sent_logp_threshold, length_norm,
-                       early_exit};
+        TbsInput input{q.beams, vi, vl, out_sent, out_logp_norm, token_logp_threshold,
+                       sent_logp_threshold, length_norm, early_exit};
         {
           py::gil_scoped_release nogil;
-          if (use_gpu) trie.tbs_gpu(input); else trie.tbs(input);
+          if (q.F) trie.tbs(input);
         }
         auto end = std::chrono::high_resolution_clock::now();
-        return std::make_tuple(out_sent, out_logp_norm, marisa::get_msec(start, end));
+        return py::make_tuple(py::cast(out_sent), py::cast(out_logp_norm),
+                              marisa::get_msec(start, end));
       },
       py::arg("trie"), py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"),
       py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
@@ -219,41 +341,44 @@ PYBIND11_MODULE(flashtrie, m) {
 
   m.def(
       "bs_tbs_gpu",
-      [](Trie& trie, size_t batch_size,
-         const std::vector<std::vector<uint32_t>>& batch_beams,
-         const std::vector<std::vector<std::vector<Label>>>& batch_topk_id,
-         const std::vector<std::vector<std::vector<float>>>& batch_topk_logp,
-         float token_logp_threshold, double sent_logp_threshold,
+      [](Trie& trie, size_t batch_size, py::object batch_beams, py::object batch_topk_id,
+         py::object batch_topk_logp, float token_logp_threshold, double sent_logp_threshold,
          double length_norm, bool early_exit) {
         ctx_of(trie);  // init_tbs_gpu must have run
         if (batch_size > trie.get_max_batch_size())
           throw marisa::Exception(MARISA_BOUND_ERROR, "bs_tbs_gpu: batch_size > max_batch_size");
-        if (batch_size != batch_topk_id.size() || batch_size != batch_topk_logp.size() ||
-            batch_size != batch_beams.size())
+        if (batch_size != (size_t)ftpy::seq_len(batch_topk_id) ||
+            batch_size != (size_t)ftpy::seq_len(batch_topk_logp) ||
+            batch_size != (size_t)ftpy::seq_len(batch_beams))
           throw marisa::Exception(MARISA_CODE_ERROR, "bs_tbs_gpu: batch_size does not match the inputs");
-        std::vector<TbsInput> inputs;
-        std::vector<std::vector<std::vector<Label>>> out_sent(batch_size);
-        std::vector<std::vector<double>> out_norm(batch_size);
-        auto start = std::chrono::high_resolution_clock::now();
-        for (size_t i = 0; i < batch_size; ++i)
-          inputs.push_back(TbsInput{batch_beams[i], batch_topk_id[i], batch_topk_logp[i],
-                                    out_sent[i], out_norm[i], token_logp_threshold,
-                                    sent_logp_threshold, length_norm, early_exit});
-        {
-          py::gil_scoped_release nogil;
-          trie.tbs_gpu_batched(inputs);
-        }
-        auto end = std::chrono::high_resolution_clock::now();
-        std::vector<std::vector<double>> phase;
-        for (auto& in : inputs)
-          phase.push_back({in.t_expansion_ms, in.t_validation_ms, in.t_selection_ms,
-                           in.t_grid_overhead_ms, in.kernel_ms});
-        return std::make_tuple(out_sent, out_norm, marisa::get_msec(start, end), phase);
+        return gpu_search(trie, batch_size, nullptr, nullptr, nullptr,
+                          std::array<py::handle, 3>{batch_beams, batch_topk_id, batch_topk_logp}
+                              .data(),
+                          token_logp_threshold, sent_logp_threshold, length_norm, early_exit);
       },
       py::arg("trie"), py::arg("batch_size"), py::arg("batch_beams"),
       py::arg("batch_topk_id"), py::arg("batch_topk_logp"),
       py::arg("token_logp_threshold"), py::arg("sents_logp_threshold"),
       py::arg("length_norm"), py::arg("early_exit"));
+
+  // The conversion of one request's arguments, as the search entry points
+  // read them: (beams, ids[T][K], logps[T][K]), for tests on the CPU.
+  m.def(
+      "_convert_request",
+      [](py::object beams, py::object topk_id, py::object topk_logp, bool generic) {
+        ftpy::ReqIn q;
+        std::vector<py::object> keep;
+        if (generic) ftpy::read_request_generic(beams, topk_id, topk_logp, q);
+        else ftpy::read_any(beams, topk_id, topk_logp, q, keep);
+        py::array_t<uint32_t> ids({(py::ssize_t)q.T, (py::ssize_t)q.K});
+        py::array_t<float> lps({(py::ssize_t)q.T, (py::ssize_t)q.K});
+        for (size_t t = 0; t < q.T; ++t) {
+          std::memcpy(ids.mutable_data() + t * q.K, q.id_rows[t], q.K * 4);
+          std::memcpy(lps.mutable_data() + t * q.K, q.lp_rows[t], q.K * 4);
+        }
+        return py::make_tuple(py::cast(q.beams), ids, lps);
+      },
+      py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"), py::arg("generic") = false);
 
   m.def("load_topk_keys_and_scores", &marisa::load_topk_keys_and_scores,
         py::arg("dataset_dir"));

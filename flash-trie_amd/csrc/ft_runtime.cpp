@@ -12,8 +12,8 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
-#include <thread>
 #include <cstdio>
 #include <cstring>
 #include <limits>
@@ -21,6 +21,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/flashtrie_amd.h"
@@ -130,6 +131,11 @@ struct ft_ctx {
   // test knob: helpers never claim their slices, so the leader takes every
   // one over after its grace period
   uint32_t no_claims = 0;
+  // a streamed search's bounded wait for a request's ready word (ticks),
+  // and a delay before the host packs (microseconds): test knobs that
+  // make requests come back not ready, to be searched again staged
+  uint64_t ready_ticks = kReadyTicks;
+  uint32_t pack_delay_us = 0;
   int max_resident = 0;
   // this device's no-allocation scratch (looked up at ft_create), or null
   // with the reason in scratch_err
@@ -711,6 +717,14 @@ int ft_create(const void* image, size_t image_bytes, int device,
     const long v = std::strtol(s, nullptr, 10);
     if (v >= 0 && v < 1000000) c->head_rows = (uint32_t)v;
   }
+  if (const char* s = std::getenv("FT_READY_TICKS")) {
+    const long long v = std::strtoll(s, nullptr, 10);
+    if (v >= 0 && (unsigned long long)v <= kReadyTicks) c->ready_ticks = (uint64_t)v;
+  }
+  if (const char* s = std::getenv("FT_PACK_DELAY_US")) {
+    const long v = std::strtol(s, nullptr, 10);
+    if (v >= 0 && v <= 1000000) c->pack_delay_us = (uint32_t)v;
+  }
   *out = c;
   return FT_OK;
 }
@@ -1282,6 +1296,7 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.ready = nullptr;
   a.out_host = nullptr;
   a.stage_bytes = 0;
+  a.ready_ticks = c->ready_ticks;
   return a;
 }
 
@@ -1501,8 +1516,12 @@ void pack_stream(PackJob& j, std::pair<uint32_t, uint32_t>* tmp) {
     j.rc[r] = rc;
     publish(r, kReadyWithdrawn);
   };
+  // The launched header (D[r], in mapped memory) keeps its planned rk_off and
+  // in_bytes: the kernel copies it at its start while this thread packs, so
+  // a rewrite here could be read half old and half new.  The planned values
+  // hold every array; whether the row indices were staged travels in the
+  // ready word (kReadyRk) instead of rk_off.
   auto finish = [&](size_t r) {
-    pack_end(j.D[r], ps[r]);
     publish(r, ((unsigned long long)j.D[r].T << kReadyRowsShift) | kReadyOk |
                    (ps[r].rk_used ? kReadyRk : 0u));
   };
@@ -1623,6 +1642,7 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   job.head_rows = a.head_rows;
   job.rc.assign(batch, FT_OK);
   job.msg.resize(batch);
+  if (c->pack_delay_us) std::this_thread::sleep_for(std::chrono::microseconds(c->pack_delay_us));
   pack_stream(job, c->sort_tmp.data());
   // Each request's results once its leader has published them (kStatusDone
   // in its header, written last with a system-scope release), in the order
@@ -1637,10 +1657,19 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   std::vector<uint8_t>& got = c->req_got;
   got.assign(batch, 0);
   size_t left = batch;
+  // requests whose leader gave up waiting for their rows (the host thread
+  // was descheduled, the input pages were faulted in, ...): searched again
+  // from the staged path once this launch is over
+  std::vector<size_t> retry;
   auto take = [&](size_t r) {
     got[r] = 1;
     --left;
     if (job.rc[r]) return;  // withdrawn: its packing error is reported
+    const OutHeader* oh = (const OutHeader*)(c->h_out + c->out_stride * r);
+    if (!c->staged[r].skip && (oh->status & kStatusNotReady)) {
+      retry.push_back(r);
+      return;
+    }
     rcs[r] = unpack_one(c->h_out + c->out_stride * r, c->staged[r], true, r, results[r], tick_ms,
                         tm, &msgs[r]);
     if (rcs[r] == FT_OK && fn) fn(user, r);
@@ -1680,10 +1709,48 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   double ms = 0.0;
   if (int rc = ft_sync(c, &ms)) return drop(rc);
   tm.kernel_ms = ms;
-  if (timing) *timing = tm;
   // the results were taken here: d_out holds no batch for ft_fetch
   c->staged.clear();
   c->launched_slot.clear();
+  if (!retry.empty()) {
+    // (the streamed kernel is over: h_stage is free for ft_stage)
+    std::vector<ft_request> sub;
+    std::vector<ft_result> sres;
+    for (size_t r : retry) {
+      sub.push_back(reqs[r]);
+      sres.push_back(results[r]);
+    }
+    ft_timing st{};
+    int rc = ft_stage(c, sub.data(), sub.size());
+    if (!rc) rc = ft_launch(c);
+    if (!rc) rc = ft_fetch(c, sres.data(), sub.size(), &st);
+    const std::string why = rc ? ft_last_error() : "";
+    for (size_t i = 0; i < retry.size(); ++i) {
+      const size_t r = retry[i];
+      results[r] = sres[i];
+      if (rc && results[r].status == FT_OK) results[r].status = rc;
+      rcs[r] = results[r].status;
+      if (rcs[r]) {
+        results[r].count = 0;
+        msgs[r] = "request " + std::to_string(r) + ": not ready in the streamed search, then " +
+                  (why.empty() ? std::string(ft_strerror(rcs[r])) : why);
+      } else if (fn) {
+        fn(user, r);
+      }
+    }
+    tm.expand_ms += st.expand_ms;
+    tm.select_ms += st.select_ms;
+    tm.other_ms += st.other_ms;
+    tm.candidates += st.candidates;
+    tm.parents += st.parents;
+    tm.children += st.children;
+    tm.probes += st.probes;
+    tm.kernel_ms += st.kernel_ms;
+    c->staged.clear();
+    c->launched_slot.clear();
+    c->launched = false;
+  }
+  if (timing) *timing = tm;
   for (size_t r = 0; r < batch; ++r)  // the first packing error in request order
     if (job.rc[r]) return fail(job.rc[r], job.msg[r]);
   for (size_t r = 0; r < batch; ++r)

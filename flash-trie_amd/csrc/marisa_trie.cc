@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
 #include <memory>
 #include <queue>
@@ -385,31 +386,52 @@ void Trie::tbs_gpu_batched(std::vector<TbsInput>& inputs) const {
     o.length = rw.lens.data();
     o.tokens = rw.toks.data();
   }
-  // each request's output vectors are filled as soon as its results are
-  // in, while the rest of the batch still searches
+  // Each request's output vectors are filled as soon as its results are
+  // in, while the rest of the batch still searches.  The callback runs
+  // inside ft_search_each with the kernel still running, so nothing may
+  // unwind through it: an exception (bad_alloc from the vectors) is kept,
+  // the search runs to its end, and it is rethrown afterwards.  On any
+  // error the outputs filled so far are emptied again: a failed call
+  // leaves no partial results.
   struct Fill {
     std::vector<TbsInput>* inputs;
     TrieImpl::SearchBuffers* sb;
-  } fill{&inputs, &sb};
+    std::exception_ptr err;
+    std::vector<size_t> filled;
+  } fill{&inputs, &sb, nullptr, {}};
+  fill.filled.reserve(B);
   auto on_result = [](void* user, size_t b) {
     Fill& f = *(Fill*)user;
+    if (f.err) return;
     TbsInput& in = (*f.inputs)[b];
     if (f.sb->shapes[b].F == 0) return;  // outputs untouched
-    const ft_result& o = f.sb->res[b];
-    const size_t T = f.sb->shapes[b].T;
-    const TrieImpl::SearchBuffers::Rows& rw = f.sb->rows[b];
-    in.out_sent.resize(o.count);
-    in.out_logp_norm.assign(rw.norms.data(), rw.norms.data() + o.count);
-    for (uint32_t i = 0; i < o.count; ++i)
-      in.out_sent[i].assign(rw.toks.data() + i * T, rw.toks.data() + i * T + rw.lens[i]);
-    in.t_expansion_ms = o.device_ms[0];
-    in.t_validation_ms = 0.0;
-    in.t_selection_ms = o.device_ms[1];
-    in.t_grid_overhead_ms = o.device_ms[2];
-    in.kernel_ms = o.device_ms[3];
+    try {
+      f.filled.push_back(b);
+      const ft_result& o = f.sb->res[b];
+      const size_t T = f.sb->shapes[b].T;
+      const TrieImpl::SearchBuffers::Rows& rw = f.sb->rows[b];
+      in.out_sent.resize(o.count);
+      in.out_logp_norm.assign(rw.norms.data(), rw.norms.data() + o.count);
+      for (uint32_t i = 0; i < o.count; ++i)
+        in.out_sent[i].assign(rw.toks.data() + i * T, rw.toks.data() + i * T + rw.lens[i]);
+      in.t_expansion_ms = o.device_ms[0];
+      in.t_validation_ms = 0.0;
+      in.t_selection_ms = o.device_ms[1];
+      in.t_grid_overhead_ms = o.device_ms[2];
+      in.kernel_ms = o.device_ms[3];
+    } catch (...) {
+      f.err = std::current_exception();
+    }
   };
   const int rc = ft_search_each(t.ctx, sb.reqs.data(), B, sb.res.data(), nullptr, on_result, &fill);
-  if (rc) throw_ft(rc, "tbs_gpu_batched");
+  if (rc || fill.err) {
+    for (size_t b : fill.filled) {
+      inputs[b].out_sent.clear();
+      inputs[b].out_logp_norm.clear();
+    }
+    if (fill.err) std::rethrow_exception(fill.err);
+    throw_ft(rc, "tbs_gpu_batched");
+  }
 }
 
 std::size_t Trie::num_tries() const {

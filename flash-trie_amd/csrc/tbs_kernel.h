@@ -53,7 +53,9 @@ __host__ __device__ inline uint32_t stream_split(uint32_t head_rows, uint32_t T,
 enum : uint32_t { kCopyClaimed = 1u, kCopyDone = 2u, kCopyRk = 4u, kCopyFailed = 8u };
 constexpr uint32_t kReadyRowsShift = 8;
 constexpr uint32_t kReadyStateMask = 0xFFu;
-// How long a leader waits for its ready word (wall-clock ticks of 10 ns).
+// How long a leader waits for its ready word (wall-clock ticks of 10 ns):
+// 1 s.  A request whose word does not come in time reports
+// kStatusNotReady, and the host searches it again from the staged path.
 constexpr unsigned long long kReadyTicks = 100000000ull;
 
 // Per-request descriptor, packed by the host at the start of the staging
@@ -76,6 +78,16 @@ struct DevReq {
   uint32_t out_T;      // token stride of the output rows
 };
 static_assert(sizeof(DevReq) == 64, "DevReq layout");
+
+// A request's block, as planned, fits the stage (stage_bytes) and its
+// arrays fit the block.  The host and the kernel evaluate it alike.
+__host__ __device__ inline bool block_fits(uint64_t stage_bytes, const DevReq& d) {
+  const uint64_t T = d.T, K = d.K;
+  return d.in_off + d.in_bytes <= stage_bytes && (d.in_bytes & 15u) == 0 &&
+         d.beams_off + 4 * T <= d.in_bytes && d.kb_off + 16 * T <= d.in_bytes &&
+         d.rid_off + 4 * T * K <= d.in_bytes && d.rlp_off + 4 * T * K <= d.in_bytes &&
+         d.rk_off + 2 * T * K <= d.in_bytes;
+}
 
 struct CurRec {     // a hypothesis kept in the beam
   double s;         // f64 sum of logps
@@ -275,6 +287,9 @@ struct KArgs {
   const unsigned long long* ready;
   uint8_t* out_host;
   uint64_t stage_bytes;
+  // how long a leader (or helper 1) waits for a ready word, in wall-clock
+  // ticks: kReadyTicks, or less when a test asks for it
+  uint64_t ready_ticks;
 };
 
 // LOUDS directory of the trie's shape: for every node v in breadth-first

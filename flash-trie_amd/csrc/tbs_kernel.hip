@@ -1310,7 +1310,7 @@ __device__ __forceinline__ unsigned long long wait_ready(const KArgs& a, uint32_
           (((uint32_t)v & (kReadyOk | kReadyWithdrawn)) ||
            ((uint32_t)v >> kReadyRowsShift) >= need))
         break;
-      if (wall_clock64() - t0 > kReadyTicks) {
+      if (wall_clock64() - t0 > a.ready_ticks) {
         v = 0;
         break;
       }
@@ -1377,15 +1377,6 @@ __device__ __forceinline__ void stage_copy(const KArgs& a, uint64_t in_off, cons
   __syncthreads();
 }
 
-// The planned block fits the stage and its arrays fit the block.
-__device__ __forceinline__ bool block_fits(const KArgs& a, const DevReq& d) {
-  const uint64_t T = d.T, K = d.K;
-  return d.in_off + d.in_bytes <= a.stage_bytes && (d.in_bytes & 15u) == 0 &&
-         d.beams_off + 4 * T <= d.in_bytes && d.kb_off + 16 * T <= d.in_bytes &&
-         d.rid_off + 4 * T * K <= d.in_bytes && d.rlp_off + 4 * T * K <= d.in_bytes &&
-         d.rk_off + 2 * T * K <= d.in_bytes;
-}
-
 // Rows [h0, h1) of the request's block with their key bounds (with `head`,
 // everything before the bounds too: the length-norm table and beam widths)
 // and, when the ready word `v` carries kReadyRk, the proposal indices of
@@ -1430,7 +1421,7 @@ __device__ __forceinline__ bool stage_in(const KArgs& a, uint32_t req, const Dev
   const bool ok = (v >> 32) == a.epoch && !((uint32_t)v & kReadyWithdrawn) &&
                   (final ? rows == d.T : ((uint32_t)v & kReadyPart) && rows >= split &&
                                              rows < d.T);
-  if (!ok || !block_fits(a, d)) {
+  if (!ok || !block_fits(a.stage_bytes, d)) {
     if (threadIdx.x == 0) {
       st_dev(&((Ctl*)(ws + a.lay.ctl))->go, tag | kGoExit);
       OutHeader* oh = (OutHeader*)(a.out_host + (uint64_t)req * a.out_stride);
@@ -1468,7 +1459,7 @@ __device__ __forceinline__ void helper_copy(const KArgs& a, uint32_t req, const 
   if (!mine) return;
   const unsigned long long v = wait_ready(a, req, d.T, sm);
   const bool ok = (v >> 32) == a.epoch && ((uint32_t)v & kReadyOk) &&
-                  ((uint32_t)v >> kReadyRowsShift) == d.T && block_fits(a, d);
+                  ((uint32_t)v >> kReadyRowsShift) == d.T && block_fits(a.stage_bytes, d);
   const bool rk = ((uint32_t)v & kReadyRk) != 0;
   if (ok) {
     const uint32_t rb = 4u * d.K;
@@ -1502,7 +1493,7 @@ __device__ __forceinline__ bool ensure_rows(const KArgs& a, uint32_t req, const 
       if (c >= (tag | kCopyClaimed)) {
         // helper 1 has it: wait (bounded) for its end
         const unsigned long long t0 = wall_clock64();
-        while ((uint32_t)c == kCopyClaimed && wall_clock64() - t0 <= kReadyTicks) {
+        while ((uint32_t)c == kCopyClaimed && wall_clock64() - t0 <= a.ready_ticks) {
           __builtin_amdgcn_s_sleep(2);
           c = ld_relaxed(&ctl->copy);
         }
@@ -2027,8 +2018,9 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   const uint32_t tid = threadIdx.x;
   if (g >= a.wgs) return;
 
-  // (a streamed request's header is final at the launch but for rk_off,
-  // which stage_in reads once the block is packed)
+  // (a streamed request's header is final at the launch: the host never
+  // rewrites it, and whether its row indices are staged comes with the
+  // ready words)
   const DevReq d = a.reqs[req];
   uint8_t* ws = a.ws + (uint64_t)req * a.ws_stride;
   if (d.flags & kReqSkip) {
@@ -2386,12 +2378,16 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         __builtin_amdgcn_s_sleep(2);
       }
       uint32_t n_stolen = 0;
-      if (pending_any) {
+      // (thread 0 alone knows whether helper 1 is copying: the takeover
+      // runs when any slot is still pending or helper 1 copies)
+      if (__syncthreads_or(pending_any || copying1)) {
         if (tid == 0) sm.n_stolen = 0;
         __syncthreads();
-        // raise every unclaimed word: a slice whose word this raises is
-        // taken over here; one a helper raised first stays the helper's
-        if (tid < nh && atomicMax(&claims[tid + 1], mygo) < mygo) {
+        // raise every unclaimed word (helper 1's alone when only it is
+        // copying): a slice whose word this raises is taken over here; one
+        // a helper raised first stays the helper's
+        if (tid < nh && (pending_any || tid == 0) &&
+            atomicMax(&claims[tid + 1], mygo) < mygo) {
           const uint32_t k = atomicAdd(&sm.n_stolen, 1u);
           sm.stolen[k] = (uint16_t)(tid + 1);
         }

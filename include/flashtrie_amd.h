@@ -222,18 +222,20 @@ int ft_search_each(ft_ctx* ctx, const ft_request* reqs, size_t batch,
 
 /* ft_search without allocating: no hipMalloc, hipHostMalloc or hipFree,
  * and no ft_reserve needed.  It has no counterpart in the reference; it is
- * for callers that cannot allocate (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  The staged requests,
- * outputs and workspace slots of the batch live in one device array of
- * FT_NOALLOC_SCRATCH_BYTES per device, which the library holds from
- * ft_create until the process ends; host packing uses static buffers.  A
- * batch that needs more (the workspace of a request grows with
- * beam x topk: batch 1 at beam = topk = 1000 fits, batch 8 does at beam =
- * topk = 350) returns FT_E_LIMIT; at most 64 requests per call.  Results
- * are identical to ft_search's.  Calls in one process are serialised (they
- * share the array, which keeps the last call's contents; the control
- * blocks are cleared on every call); calls from different processes get
- * their own copies. */
+ * for callers that must not allocate (tight serving loops, harnesses that
+ * forbid hipMalloc).  The staged requests, outputs and workspace slots of
+ * the batch live in one device array of FT_NOALLOC_SCRATCH_BYTES per
+ * device, which the library holds from ft_create until the process ends;
+ * host packing uses static buffers.  A batch that needs more (the
+ * workspace of a request grows with beam x topk: batch 1 at beam = topk =
+ * 1000 fits, batch 8 does at beam = topk = 350) returns FT_E_LIMIT; at
+ * most 64 requests per call.  Results are identical to ft_search's.  It
+ * is a synchronous call: it copies the packed batch from pageable host
+ * memory, launches, copies the results back and waits for the context's
+ * stream, so it cannot be recorded into a HIP graph (stream capture).
+ * Calls in one process are serialised (they share the array, which keeps
+ * the last call's contents; the control blocks are cleared on every
+ * call); calls from different processes get their own copies. */
 #define FT_NOALLOC_SCRATCH_BYTES (128u << 20)
 int ft_search_noalloc(ft_ctx* ctx, const ft_request* reqs, size_t batch,
                       ft_result* results, ft_timing* timing);

@@ -208,6 +208,11 @@ int main() {
     const int rc2 = plan_batch(reqs.data(), n, lim, H2.data(), H2.size(), st2.data(), &used2,
                                &os2, &first_bad, &msg);
     CHECK(rc2 == FT_OK && used2 == used, "stream case %d: plan rc %d", c, rc2);
+    // the headers as launched: packing must leave them as they are (the
+    // kernel copies them while the host packs), and they must fit
+    std::vector<DevReq> planned((const DevReq*)H2.data(), (const DevReq*)H2.data() + n);
+    for (uint32_t r = 0; r < n; ++r)
+      CHECK(block_fits(used2, planned[r]), "stream case %d request %u: planned block", c, r);
     PackJob job;
     job.reqs = reqs.data();
     job.D = (DevReq*)H2.data();
@@ -223,16 +228,31 @@ int main() {
     for (uint32_t r = 0; r < n; ++r) {
       const bool bad = r == nan_req;
       CHECK((job.rc[r] != FT_OK) == bad, "stream case %d request %u: rc %d", c, r, job.rc[r]);
+      CHECK(std::memcmp(&job.D[r], &planned[r], sizeof(DevReq)) == 0,
+            "stream case %d request %u: the launched header was rewritten", c, r);
+      // the indices are staged (kReadyRk) iff pack_batch stages them
+      const bool rk = rc1 == FT_OK && ((const DevReq*)H.data())[r].rk_off != 0;
       const unsigned long long want =
           bad ? kReadyWithdrawn
-              : ((unsigned long long)T << kReadyRowsShift) | kReadyOk |
-                    (job.D[r].rk_off ? kReadyRk : 0u);
-      CHECK(ready[r] == (job.tag | want), "stream case %d request %u: ready word %llx", c, r,
-            ready[r]);
+              : ((unsigned long long)T << kReadyRowsShift) | kReadyOk | (rk ? kReadyRk : 0u);
+      if (rc1 == FT_OK || bad)
+        CHECK(ready[r] == (job.tag | want), "stream case %d request %u: ready word %llx", c, r,
+              ready[r]);
     }
     if (nan_req == n) {
       CHECK(rc1 == FT_OK, "stream case %d: pack_batch rc %d", c, rc1);
-      CHECK(std::memcmp(H.data(), H2.data(), used) == 0, "stream case %d: blocks differ", c);
+      // the blocks equal pack_batch's; its headers differ only in rk_off and
+      // in_bytes, which it trims when no indices are staged
+      const size_t hdr = align_up(n * sizeof(DevReq), 256);
+      CHECK(std::memcmp(H.data() + hdr, H2.data() + hdr, used - hdr) == 0,
+            "stream case %d: blocks differ", c);
+      for (uint32_t r = 0; r < n; ++r) {
+        DevReq x = ((const DevReq*)H.data())[r], y = planned[r];
+        CHECK(x.rk_off == 0 || x.rk_off == y.rk_off, "stream case %d: rk_off", c);
+        x.rk_off = y.rk_off = 0;
+        x.in_bytes = y.in_bytes = 0;
+        CHECK(std::memcmp(&x, &y, sizeof x) == 0, "stream case %d: headers differ", c);
+      }
       ++streamed;
     } else {
       CHECK(rc1 == FT_E_INPUT, "stream case %d: pack_batch rc %d", c, rc1);

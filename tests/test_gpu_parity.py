@@ -126,6 +126,47 @@ def test_c1_batched_numpy(ft, c1):
             assert_same_results((sents, norms[i, :n]), want, f"batch {b0}+{i}")
 
 
+def test_bs_tbs_gpu_argument_forms(ft, c1):
+    """bs_tbs_gpu reads lists, tuples and numpy arrays (a [B][T][K] batch,
+    per-request [T][K] arrays, float64 logps, int64 ids) in place: every
+    form gives the same results as the reference's nested lists, and those
+    equal the oracle's."""
+    t, o, ids, lp = c1
+    B = 8
+    beams = [[10] * 8] * B
+    for b0 in range(0, 32, B):
+        bi, bl = ids[b0:b0 + B], lp[b0:b0 + B]
+        print("argument forms, requests", b0, flush=True)
+        forms = {
+            "lists": (beams, bi.tolist(), bl.tolist()),
+            "np3d": (np.full((B, 8), 10, np.uint32), bi, bl),
+            "np2d_each": (beams, list(bi), list(bl)),
+            "f64_i64": (beams, bi.astype(np.int64), bl.astype(np.float64)),
+            "tuples": (tuple(map(tuple, beams)), tuple(r.tolist() for r in bi),
+                       tuple(r.tolist() for r in bl)),
+        }
+        ref = None
+        for name, (bb, ii, ll) in forms.items():
+            sents, norms, ms, phase = ft.bs_tbs_gpu(t, B, bb, ii, ll, -10.0, -40.0, 5.0,
+                                                    False)
+            assert isinstance(sents, list) and isinstance(norms[0], list), name
+            assert ms >= 0 and len(phase) == B and len(phase[0]) == 5, name
+            if ref is None:
+                ref = (sents, norms)
+                for i in range(B):
+                    want = o.tbs([10] * 8, bi[i], bl[i], -10.0, -40.0, 5.0, False)
+                    assert_same_results((sents[i], norms[i]), want, f"{b0}+{i}")
+            else:
+                assert sents == ref[0], name
+                assert [np.asarray(n).view(np.uint64).tolist() for n in norms] == \
+                    [np.asarray(n).view(np.uint64).tolist() for n in ref[1]], name
+    # tbs(use_gpu=True) with numpy arrays
+    for r in range(4):
+        got = ft.tbs(t, np.full(8, 10), ids[r], lp[r], -10.0, -40.0, 5.0, False, True)
+        want = o.tbs([10] * 8, ids[r], lp[r], -10.0, -40.0, 5.0, False)
+        assert_same_results(got[:2], want, f"tbs request {r}")
+
+
 def test_c1_as_written_oracle(ft, c1, po):
     t, o, ids, lp = c1
     for r in range(10):
@@ -310,6 +351,33 @@ def test_streamed_batches(ft, c1, early):
     for i in range(8):
         want = o.tbs([10] * 8, ids[i], lp[i], -10.0, -40.0, 5.0, early)
         assert_same_results((s[i], n[i]), want, f"after the withdrawn batch, {i}")
+
+
+@pytest.mark.parametrize("head_rows", ["0", "3"])
+def test_not_ready_requests_are_searched_again(ft, po, monkeypatch, head_rows):
+    # The host packs 3 ms late and the kernel waits 1 us for a request's
+    # rows: every leader (and helper 1, which copies the later rows) gives
+    # up after its bounded wait and reports the request not ready, and the
+    # host searches those requests again from the staged path.  The results
+    # are the oracle's; the next call on the same context is sound.
+    monkeypatch.setenv("FT_READY_TICKS", "100")
+    monkeypatch.setenv("FT_PACK_DELAY_US", "3000")
+    monkeypatch.setenv("FT_HEAD_ROWS", head_rows)
+    toks, offs = ft.synth_keys(C1["n"], C1["vocab"], C1["lmin"], C1["lmax"],
+                               C1["s"], C1["seed"])
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=8, topk=32, steps=8, beams=10,
+                  inter=1024)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 16, C1["vocab"], 8, 32, 8, 0.3, 2.0, True, 0)
+    for b0 in (0, 8):
+        print("not-ready batch", b0, "head_rows", head_rows, flush=True)
+        s, n, _, _ = ft.bs_tbs_gpu(t, 8, [[10] * 8] * 8, ids[b0:b0 + 8], lp[b0:b0 + 8],
+                                   -10.0, -40.0, 5.0, b0 == 8)
+        for i in range(8):
+            want = o.tbs([10] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, b0 == 8)
+            assert_same_results((s[i], n[i]), want, f"not ready {b0}+{i}")
+    got = ft.tbs(t, [10] * 8, ids[0], lp[0], -10.0, -40.0, 5.0, False, True)
+    assert_same_results(got[:2], o.tbs([10] * 8, ids[0], lp[0], -10.0, -40.0, 5.0, False))
 
 
 def test_history_limit_is_an_error(ft):
