@@ -9,6 +9,7 @@ Outputs, next to this file:
 Run ``python flash-trie_amd/build.py`` or call ``build()``.
 """
 
+import hashlib
 import os
 import subprocess
 import sys
@@ -56,6 +57,47 @@ def _run(cmd):
     return out
 
 
+# Every file the libraries are built from: their sources and headers, the
+# public headers, and this recipe (its flags).
+def _source_files():
+    files = [os.path.abspath(__file__)]
+    for d in (CSRC, INC):
+        for dirpath, dirnames, names in os.walk(d):
+            dirnames[:] = sorted(x for x in dirnames if not x.startswith((".", "__")))
+            files += [os.path.join(dirpath, n) for n in sorted(names)
+                      if n.endswith((".h", ".hip", ".cpp", ".cc"))]
+    return files
+
+
+def source_id():
+    """Build id of the current sources: sha256 (16 hex digits) over every
+    source file's path (relative to the repository) and bytes.  Each built
+    library carries the id of the sources it was built from."""
+    h = hashlib.sha256()
+    for f in _source_files():
+        h.update(os.path.relpath(f, ROOT).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
+ID_TAG = b"FT_BUILD_ID="
+
+
+def built_id(path):
+    """The build id embedded in a built library (None when absent)."""
+    try:
+        with open(path, "rb") as fh:
+            data = fh.read()
+    except OSError:
+        return None
+    i = data.find(ID_TAG)
+    if i < 0:
+        return None
+    return data[i + len(ID_TAG):i + len(ID_TAG) + 16].decode("ascii", "replace")
+
+
 def _pybind_includes():
     import pybind11
     return ["-I" + pybind11.get_include(),
@@ -64,6 +106,7 @@ def _pybind_includes():
 
 def build(verbose=False):
     os.makedirs(OBJ, exist_ok=True)
+    bid = ["-DFT_BUILD_ID=\"" + source_id() + "\""]
     hip_objs = {
         "tbs_kernel.hip": os.path.join(OBJ, "tbs_kernel.o"),
         "ft_runtime.cpp": os.path.join(OBJ, "ft_runtime.o"),
@@ -80,14 +123,14 @@ def build(verbose=False):
     jobs = []
     for src, obj in hip_objs.items():
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        jobs.append([HIPCC] + HIP_FLAGS + lang + ["-c", os.path.join(CSRC, src),
-                                                  "-o", obj])
+        jobs.append([HIPCC] + HIP_FLAGS + bid + lang + ["-c", os.path.join(CSRC, src),
+                                                        "-o", obj])
     for src, obj in host_objs.items():
-        jobs.append([CXX] + CXX_FLAGS + ["-c", os.path.join(CSRC, src),
-                                         "-o", obj])
+        jobs.append([CXX] + CXX_FLAGS + bid + ["-c", os.path.join(CSRC, src),
+                                               "-o", obj])
     jobs.append([HIPCC] + HIP_FLAGS + ["-x", "hip", os.path.join(CSRC, "copy_calib.hip"),
                                        "-o", COPY_CALIB])
-    jobs.append([CXX] + CXX_FLAGS + _pybind_includes() +
+    jobs.append([CXX] + CXX_FLAGS + bid + _pybind_includes() +
                 ["-fvisibility=hidden", "-c", os.path.join(CSRC, "bindings.cc"),
                  "-o", bind_obj])
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
@@ -112,7 +155,11 @@ def build(verbose=False):
 
 
 def built():
-    return all(os.path.exists(p) for p in (LIB_AMD, LIB_MARISA, PYMOD))
+    """True when the three libraries exist and were built from the current
+    sources (their embedded build ids equal source_id()); a stale build is
+    rebuilt, never loaded."""
+    sid = source_id()
+    return all(built_id(p) == sid for p in (LIB_AMD, LIB_MARISA, PYMOD))
 
 
 if __name__ == "__main__":

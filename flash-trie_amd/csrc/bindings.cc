@@ -184,8 +184,25 @@ py::tuple gpu_search(Trie& trie, size_t B, const py::object* one_beams,
 
 }  // namespace
 
+#ifndef FT_BUILD_ID
+#define FT_BUILD_ID "unknown"
+#endif
+// the build id tag of this module (see ft_build_id)
+extern "C" __attribute__((used, visibility("default"))) const char ft_module_build_id[] =
+    "FT_BUILD_ID=" FT_BUILD_ID;
+
 PYBIND11_MODULE(flashtrie, m) {
   m.doc() = "MI355X trie beam search (drop-in for the reference flashtrie module)";
+  // the build ids of this module and of the C ABI library it loaded: the
+  // same unless a library was rebuilt alone
+  m.def("build_id", []() {
+    if (std::strcmp(ft_build_id(), ft_module_build_id + 12) != 0)
+      throw marisa::Exception(MARISA_STATE_ERROR,
+                              std::string("build_id: the module (") + (ft_module_build_id + 12) +
+                                  ") and libflashtrie_amd.so (" + ft_build_id() +
+                                  ") come from different builds");
+    return std::string(ft_build_id());
+  });
   py::register_exception<marisa::Exception>(m, "MarisaError", PyExc_RuntimeError);
 
   py::class_<Trie>(m, "Trie")

@@ -595,7 +595,16 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   return FT_OK;
 }
 
+#ifndef FT_BUILD_ID
+#define FT_BUILD_ID "unknown"
+#endif
+// The build id (a hash of the sources the library was built from), behind
+// a tag the build recipe finds in the binary.
+static const char g_build_id[] = "FT_BUILD_ID=" FT_BUILD_ID;
+
 extern "C" {
+
+const char* ft_build_id(void) { return g_build_id + 12; }
 
 const char* ft_last_error(void) { return g_err.c_str(); }
 

@@ -21,6 +21,12 @@
 #include "marisa_format.h"
 #include "trie_impl.h"
 
+#ifndef FT_BUILD_ID
+#define FT_BUILD_ID "unknown"
+#endif
+// the build id tag (see ft_build_id), kept in the binary
+extern "C" __attribute__((used)) const char ft_marisa_build_id[] = "FT_BUILD_ID=" FT_BUILD_ID;
+
 namespace marisa {
 
 namespace {

@@ -248,6 +248,11 @@ void ft_destroy(ft_ctx* ctx);
 
 const char* ft_strerror(int code);
 
+/* The id of the sources this library was built from (16 hex digits of a
+ * sha256 over them); no counterpart in the reference.  Benchmarks and
+ * profiles record it, so a figure names the exact build it measured. */
+const char* ft_build_id(void);
+
 /* Thread-local text of the most recent error raised on this thread. */
 const char* ft_last_error(void);
 
