@@ -225,6 +225,32 @@ PYBIND11_MODULE(flashtrie, m) {
              t.build(ks, 1 | MARISA_TEXT_TAIL | MARISA_LABEL_ORDER | MARISA_DEFAULT_CACHE);
            },
            py::arg("token_rows"))
+      // beyond the reference module (its C++ Trie has them,
+      // lib/marisa/trie.cc:33-43, 57-67, 78-86): a trie from a buffer used
+      // in place (kept alive with the Trie), or from / to a descriptor
+      .def(
+          "map",
+          [](Trie& t, py::buffer b) {
+            py::buffer_info bi = b.request();
+            const size_t n = (size_t)bi.size * (size_t)bi.itemsize;
+            if (bi.ndim > 1 && !(bi.strides.back() == bi.itemsize))
+              throw marisa::Exception(MARISA_CODE_ERROR, "map: the buffer must be contiguous");
+            py::gil_scoped_release nogil;
+            t.map(bi.ptr, n);
+          },
+          py::arg("buffer"), py::keep_alive<1, 2>())
+      .def("read",
+           [](Trie& t, int fd) {
+             py::gil_scoped_release nogil;
+             t.read(fd);
+           },
+           py::arg("fd"))
+      .def("write",
+           [](const Trie& t, int fd) {
+             py::gil_scoped_release nogil;
+             t.write(fd);
+           },
+           py::arg("fd"))
       .def("total_size", &Trie::total_size)
       .def("num_tries", &Trie::num_tries)
       .def("num_keys", &Trie::num_keys)

@@ -18,6 +18,7 @@
 #include "image_builder.h"
 
 #include <algorithm>
+#include <cerrno>
 #include <cstdlib>
 #include <cstring>
 #include <numeric>
@@ -36,7 +37,9 @@ static inline uint64_t align_up(uint64_t v, uint64_t a) {
 ImageBlob::~ImageBlob() { clear(); }
 
 void ImageBlob::clear() {
-  if (mapped_) {
+  if (borrowed_) {
+    // the caller's memory
+  } else if (mapped_) {
     if (data_) ::munmap(data_, size_);
   } else {
     std::free(data_);
@@ -44,6 +47,46 @@ void ImageBlob::clear() {
   data_ = nullptr;
   size_ = 0;
   mapped_ = false;
+  borrowed_ = false;
+}
+
+void ImageBlob::borrow(const void* p, size_t n) {
+  clear();
+  data_ = (uint8_t*)p;
+  size_ = n;
+  borrowed_ = true;
+}
+
+bool ImageBlob::allocate_bytes(size_t n) {
+  clear();
+  data_ = (uint8_t*)std::aligned_alloc(256, ((n ? n : 1) + 255) / 256 * 256);
+  if (!data_) return false;
+  size_ = n;
+  return true;
+}
+
+bool read_exact(int fd, void* p, size_t n) {
+  uint8_t* d = (uint8_t*)p;
+  while (n) {
+    const ssize_t r = ::read(fd, d, std::min<size_t>(n, 1u << 30));
+    if (r < 0 && errno == EINTR) continue;
+    if (r <= 0) return false;
+    d += r;
+    n -= (size_t)r;
+  }
+  return true;
+}
+
+bool write_all(int fd, const void* p, size_t n) {
+  const uint8_t* d = (const uint8_t*)p;
+  while (n) {
+    const ssize_t r = ::write(fd, d, std::min<size_t>(n, 1u << 30));
+    if (r < 0 && errno == EINTR) continue;
+    if (r <= 0) return false;
+    d += r;
+    n -= (size_t)r;
+  }
+  return true;
 }
 
 bool ImageBlob::read_file(const char* path, std::string* err) {

@@ -10,8 +10,9 @@
 
 namespace ftamd {
 
-// An image blob: owned (256-byte aligned heap memory) or a private
-// read-write mapping of an image file (page aligned; writes stay private).
+// An image blob: owned (256-byte aligned heap memory), a private
+// read-write mapping of an image file (page aligned; writes stay private),
+// or memory the caller owns and keeps alive (borrowed; never freed here).
 class ImageBlob {
  public:
   ImageBlob() = default;
@@ -27,6 +28,7 @@ class ImageBlob {
     std::swap(data_, o.data_);
     std::swap(size_, o.size_);
     std::swap(mapped_, o.mapped_);
+    std::swap(borrowed_, o.borrowed_);
   }
   // Allocates a zeroed blob laid out for the given sizes and fills the header.
   bool allocate(uint64_t num_nodes, uint64_t tail_len);
@@ -37,6 +39,10 @@ class ImageBlob {
   // Maps a whole file (private, copy-on-write): the pages are read on first
   // use and shared with the page cache.
   bool map_file(const char* path, std::string* err);
+  // Uses n bytes at p in place (the caller keeps them alive and unchanged).
+  void borrow(const void* p, size_t n);
+  // An owned, uninitialised blob of n bytes (256-byte aligned).
+  bool allocate_bytes(size_t n);
   bool mapped() const { return mapped_; }
   void clear();
 
@@ -63,7 +69,14 @@ class ImageBlob {
   uint8_t* data_ = nullptr;
   size_t size_ = 0;
   bool mapped_ = false;
+  bool borrowed_ = false;
 };
+
+// Reads exactly n bytes from a descriptor (retrying short reads and EINTR);
+// false at end of file or on an error.
+bool read_exact(int fd, void* p, size_t n);
+// Writes n bytes to a descriptor (retrying short writes and EINTR).
+bool write_all(int fd, const void* p, size_t n);
 
 // Builds the trie of `nkeys` keys (key i = toks[offs[i] .. offs[i+1])) with
 // the reference's node numbering (MARISA BFS, label order, path compression:

@@ -165,6 +165,42 @@ bool read_packed(Reader& r, Packed* f, const char* what) {
 
 }  // namespace
 
+bool read_marisa_stream(int fd, const uint8_t head[16], std::vector<uint8_t>* out,
+                        std::string* err) {
+  out->assign(head, head + 16);
+  auto need = [&](uint64_t n, const char* what) {
+    const size_t o = out->size();
+    out->resize(o + (size_t)n);
+    if (!read_exact(fd, out->data() + o, (size_t)n)) {
+      *err = std::string("read: the stream ends in ") + what;
+      return false;
+    }
+    return true;
+  };
+  // a Vector: its byte count, then the bytes padded to 8
+  auto vec = [&](const char* what) {
+    if (!need(8, what)) return false;
+    uint64_t total;
+    std::memcpy(&total, out->data() + out->size() - 8, 8);
+    if (total > (1ull << 44)) {
+      *err = std::string("read: implausible size of ") + what;
+      return false;
+    }
+    return need(total + (8 - total % 8) % 8, what);
+  };
+  // a BitVector: units, size and count of ones, rank and select samples
+  auto bits = [&](const char* what) {
+    return vec(what) && need(8, what) && vec(what) && vec(what) && vec(what);
+  };
+  // a FlatVector: units, value size and mask, value count
+  auto packed = [&](const char* what) { return vec(what) && need(16, what); };
+  // the order LoudsTrie writes them in (louds-trie.cc:747-762)
+  return bits("LOUDS bits") && bits("terminal flags") && bits("link flags") &&
+         vec("label bases") && packed("label extras") && packed("link extras") &&
+         vec("tail") && bits("tail end flags") && vec("cache") &&
+         need(8, "level-1 node count and config flags");
+}
+
 bool is_marisa_file(const void* data, size_t size) {
   return data && size >= 16 && std::memcmp(data, kHeader, 16) == 0;
 }

@@ -30,6 +30,15 @@ bool is_marisa_file(const void* data, size_t size);
 bool image_from_marisa(const uint8_t* data, size_t size, ImageBlob* out,
                        std::string* err, int threads = 0);
 
+// Reads one MARISA trie file from a descriptor whose first 16 bytes (the
+// header, already read) are `head`: exactly the file's bytes, section by
+// section (every Vector carries its byte count), so a stream can hold more
+// after it -- as the reference's Reader reads one trie (trie.cc:57-67).
+// The bytes go to *out for image_from_marisa.  False with *err set on a
+// short read or an implausible section size.
+bool read_marisa_stream(int fd, const uint8_t head[16], std::vector<uint8_t>* out,
+                        std::string* err);
+
 // Encodes an image as the MARISA trie file the reference writes for its keys
 // when every key has weight 1 (the Python build's keyset) and the config is
 // num_tries = 1 | MARISA_TEXT_TAIL | MARISA_LABEL_ORDER | MARISA_NORMAL_CACHE

@@ -268,6 +268,66 @@ void Trie::load(const char* filename) { open_trie(filename, false, &impl_); }
 
 void Trie::mmap(const char* filename) { open_trie(filename, true, &impl_); }
 
+void Trie::map(const void* ptr, std::size_t size) {
+  if (!ptr && size) throw Exception(MARISA_NULL_ERROR, "map: null pointer");
+  auto fresh = std::unique_ptr<TrieImpl>(new TrieImpl());
+  std::string err;
+  if (ftamd::is_marisa_file(ptr, size)) {
+    if (!ftamd::image_from_marisa((const uint8_t*)ptr, size, &fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, "map: " + err);
+  } else {
+    // an image is used in place when its arrays are aligned, else copied
+    if ((uintptr_t)ptr % 16 == 0) {
+      fresh->img.borrow(ptr, size);
+    } else if (!fresh->img.assign(ptr, size)) {
+      throw Exception(MARISA_MEMORY_ERROR, "map: out of memory");
+    }
+    if (!ftamd::validate_image(fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, "map: " + err);
+  }
+  impl_.swap(fresh);
+}
+
+void Trie::read(int fd) {
+  if (fd == -1) throw Exception(MARISA_CODE_ERROR, "read: fd == -1");
+  auto fresh = std::unique_ptr<TrieImpl>(new TrieImpl());
+  std::string err;
+  uint8_t head[sizeof(ft_image_header)];
+  if (!ftamd::read_exact(fd, head, 16))
+    throw Exception(MARISA_IO_ERROR, "read: the stream ends before a trie header");
+  if (ftamd::is_marisa_file(head, 16)) {
+    std::vector<uint8_t> bytes;
+    if (!ftamd::read_marisa_stream(fd, head, &bytes, &err))
+      throw Exception(MARISA_IO_ERROR, err);
+    if (!ftamd::image_from_marisa(bytes.data(), bytes.size(), &fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, "read: " + err);
+  } else {
+    if (std::memcmp(head, FT_IMAGE_MAGIC, 8) != 0)
+      throw Exception(MARISA_FORMAT_ERROR, "read: neither a MARISA trie file nor a trie image");
+    if (!ftamd::read_exact(fd, head + 16, sizeof(head) - 16))
+      throw Exception(MARISA_IO_ERROR, "read: the stream ends in the image header");
+    ft_image_header h;
+    std::memcpy(&h, head, sizeof(h));
+    if (h.total_bytes < sizeof(h) || h.total_bytes > (1ull << 44))
+      throw Exception(MARISA_FORMAT_ERROR, "read: implausible image size");
+    if (!fresh->img.allocate_bytes((size_t)h.total_bytes))
+      throw Exception(MARISA_MEMORY_ERROR, "read: out of memory");
+    std::memcpy(fresh->img.data(), head, sizeof(h));
+    if (!ftamd::read_exact(fd, fresh->img.data() + sizeof(h), (size_t)h.total_bytes - sizeof(h)))
+      throw Exception(MARISA_IO_ERROR, "read: the stream ends inside the image");
+    if (!ftamd::validate_image(fresh->img, &err))
+      throw Exception(MARISA_FORMAT_ERROR, "read: " + err);
+  }
+  impl_.swap(fresh);
+}
+
+void Trie::write(int fd) const {
+  require_trie(impl_.get());
+  if (fd == -1) throw Exception(MARISA_CODE_ERROR, "write: fd == -1");
+  if (!ftamd::write_all(fd, impl_->img.data(), impl_->img.size()))
+    throw Exception(MARISA_IO_ERROR, "write: failed on the descriptor");
+}
+
 void Trie::save(const char* filename) const {
   require_trie(impl_.get());
   if (!filename) throw Exception(MARISA_NULL_ERROR, "save: null filename");

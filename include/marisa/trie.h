@@ -44,6 +44,15 @@ class Trie {
   void mmap(const char* filename);
   void save(const char* filename) const;
   void save_marisa(const char* filename) const;
+  // The same from memory and descriptors (lib/marisa/trie.cc:33-43,
+  // 57-67, 78-86): map uses a trie image at ptr in place (the caller keeps
+  // it alive; a MARISA file there is converted); read takes one trie from
+  // the descriptor's current position, reading exactly its bytes; write
+  // writes what save does.  A null ptr with size > 0 throws
+  // MARISA_NULL_ERROR, fd == -1 MARISA_CODE_ERROR.
+  void map(const void* ptr, std::size_t size);
+  void read(int fd);
+  void write(int fd) const;
 
   void init_tbs_gpu(size_t max_batch_size, size_t max_num_topk = 1024,
                     size_t max_num_outpos = 64, size_t max_num_out_beams = 8192,
