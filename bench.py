@@ -139,7 +139,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--child-index", default="records", choices=["records", "louds"],
                    help="child ranges from the node records or from the LOUDS "
-                        "rank/select directory")
+                        "rank/select directory (switched off: its kernel faulted "
+                        "once and the cause is not found)")
     return p.parse_args()
 
 

@@ -8,8 +8,11 @@
 
 namespace ftk {
 
-// Largest K whose proposal row is staged in LDS (10 bytes per proposal).
+// Largest K whose proposal row is staged in LDS (8 bytes per proposal);
+// a longer row is searched where it is staged, in device memory.
 constexpr uint32_t kMaxLdsTopk = 4096;
+// Largest K: a candidate's position in its row is packed into 16 bits.
+constexpr uint32_t kMaxTopk = 65535;
 // Parent index and proposal index are packed into 16 bits each.
 constexpr uint32_t kMaxBeams = 65535;
 constexpr uint32_t kNoHist = 0xFFFFFFFFu;

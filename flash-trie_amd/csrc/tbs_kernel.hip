@@ -99,6 +99,10 @@ struct alignas(16) Smem {
   // where the leader writes its results: out_host's block of the request,
   // or null for `out` (kept here rather than in registers through the steps)
   unsigned long long res_host;
+  // a row longer than the LDS row arrays (K > kMaxLdsTopk) stays in the
+  // device stage: the step's row there (tokens, logps), read only by the
+  // lookups of such a row
+  unsigned long long grow_id, grow_lp;
   // expansion: the current proposal row in ascending token order
   alignas(16) uint32_t row_id[kMaxLdsTopk];
   float row_lp[kMaxLdsTopk];
@@ -984,6 +988,18 @@ struct StepView {
   bool one_each;
 };
 
+// Position of tok in a sorted row held in the device stage (a row longer
+// than the LDS row arrays), or -1.  Device-coherent loads: a streamed
+// search's leader copied the row to the stage during this launch.
+__device__ __forceinline__ int grow_find(const uint32_t* rid, uint32_t K, uint32_t tok) {
+  uint32_t lo = 0, hi = K;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (ld_relaxed(rid + mid) < tok) lo = mid + 1; else hi = mid;
+  }
+  return (lo < K && ld_relaxed(rid + lo) == tok) ? (int)lo : -1;
+}
+
 // Expands the step's work items: each is (parent, child) for a scanned
 // parent, (parent, proposal) for a searched or hashed parent, or the single
 // pending token of a link parent.  Items go out in chunks of 64 (one per
@@ -1062,6 +1078,8 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
       md &= kModeMask;
       int pos = -1;
       bool have_child = false, label_sel = false;
+      // the token a link parent or a scanned child looks up in the row
+      uint32_t ftok = kNoToken;
       if (md == M_LP_NEXT || md == M_LP_SEL) {
         // the leader reads the next pending token of a link parent that
         // stays one (for its emit) while the row is searched
@@ -1070,7 +1088,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
           const uint32_t tc = sm.p_lp[pj];
           if (tc != kNoCursor) xtok = a.tail[tc + 1u];
         }
-        pos = row_find(sm, K, aux, hashed);
+        ftok = aux;
         cnode = lds_par ? sm.p_node[pj] : ld_relaxed(&v.pnode[pj]);
         if (xtok != kNoToken) sm.x_tok[pj] = xtok;
       } else if (md == M_SCAN) {
@@ -1078,16 +1096,25 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
         cnode = c0 + q;
         const uint32_t lw = a.labels[cnode];
         ++my_children;
-        pos = row_find(sm, K, lw & kTokMask, hashed);
+        ftok = lw & kTokMask;
         have_child = true;
         label_sel = (lw & kSlotSel) && depth_ok;
       } else if (md == M_SEARCH || md == M_HASH) {
         pos = (int)q;
       }
+      if (ftok != kNoToken)
+        pos = K > kMaxLdsTopk ? grow_find((const uint32_t*)sm.grow_id, K, ftok)
+                              : row_find(sm, K, ftok, hashed);
       if (pos >= 0) {
-        const float x = sm.row_lp[pos];
+        float x;
+        if (K > kMaxLdsTopk) {
+          x = __uint_as_float(ld_relaxed((const uint32_t*)sm.grow_lp + pos));
+          tok = ld_relaxed((const uint32_t*)sm.grow_id + pos);
+        } else {
+          x = sm.row_lp[pos];
+          tok = sm.row_id[pos];
+        }
         k = (uint32_t)pos;
-        tok = sm.row_id[pos];
         const double ps = lds_par ? sm.p_s[pj] : ld_cur(&v.cur[pj]).s;
         // thresholds in double, `<=` drops (louds-trie.cc:87-90)
         const bool low = ((double)x <= (double)v.tok_thr) ||
@@ -1636,15 +1663,22 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     sv.keep_lds_max = 0;
     sv.one_each = false;
     // the step's row (into the row hash too: emptied after the previous
-    // step) and parent table in one round of reads
+    // step) and parent table in one round of reads; a row longer than the
+    // LDS row arrays is searched where it is staged
     const bool hashed = d.K <= kRowHashMaxK;
     const bool lds_par = n_par <= (uint32_t)kBlock;
     const uint64_t ro = (uint64_t)t * d.K;
-    const uint32_t nload = max(d.K, lds_par ? n_par + 1u : 0u);
+    const bool big = d.K > kMaxLdsTopk;
+    if (big && tid == 0) {
+      sm.grow_id = (unsigned long long)(rid + ro);
+      sm.grow_lp = (unsigned long long)(rlp + ro);
+    }
+    const uint32_t Kl = big ? 0u : d.K;  // row entries loaded into LDS
+    const uint32_t nload = max(Kl, lds_par ? n_par + 1u : 0u);
     for (uint32_t i = tid; i < nload; i += kBlock) {
       uint32_t tok = 0;
       float lp = 0.0f;
-      if (i < d.K) {
+      if (i < Kl) {
         if constexpr (kStreamed) {
           tok = ld_relaxed(rid + ro + i);
           lp = __uint_as_float(ld_relaxed((const uint32_t*)rlp + ro + i));
@@ -1665,7 +1699,7 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
           sm.p_hist[i] = p.hist;
         }
       }
-      if (i < d.K) {
+      if (i < Kl) {
         sm.row_id[i] = tok;
         sm.row_lp[i] = lp;
         if (hashed) row_hash_insert(tok, i, sm);
@@ -2192,7 +2226,14 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         sm.row_lp[tid] = pf_lp;
       }
     } else {
-      load_row(rid, rlp, t, K, sm);
+      if (K <= kMaxLdsTopk) {
+        load_row(rid, rlp, t, K, sm);
+      } else if (tid == 0) {
+        // a row longer than the LDS row arrays is searched in the stage
+        // (the parent phase ends synchronised: every thread sees these)
+        sm.grow_id = (unsigned long long)(rid + (uint64_t)t * K);
+        sm.grow_lp = (unsigned long long)(rlp + (uint64_t)t * K);
+      }
     }
     const double lnf_next = lnf[t + 1];
 
@@ -2312,6 +2353,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     sv.sent_thr = d.sent_thr;
     sv.keep_lds_max = min((uint32_t)kPushCap, beams[t]);
     sv.one_each = n_cur <= (uint32_t)kBlock && sm.multi_item == 0;
+
 
     const bool shared = a.wgs > 1 && W >= a.share_min;
     if (shared) {
@@ -2624,7 +2666,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     // in LDS when the step had at most kBlock parents; the row is, unless
     // the rank scratch took it
     const bool x_ok = ncur_now <= (uint32_t)kBlock;
-    const bool row_ok = !ranks_done;
+    const bool row_ok = !ranks_done && K <= kMaxLdsTopk;
     auto emit = [&](uint32_t i, uint32_t o) {
       const NextRec c = next_in_lds ? sm.push_next[i] : nextc[i];
       const uint32_t j = c.jk >> 16, q = c.jk & 0xFFFFu;

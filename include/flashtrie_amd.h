@@ -155,7 +155,10 @@ typedef struct ft_ctx ft_ctx;
 int ft_create(const void* image, size_t image_bytes, int device,
               ft_ctx** out);
 
-/* Allocates the per-request workspace once (device + pinned host).
+/* Allocates the per-request workspace once (device + pinned host), sized
+ * for max_batch requests (init_tbs_gpu, tbs-kernels.cu:599-648).
+ *   max_topk        bounds K, the proposals per row (at most 65535)
+ *   max_steps       bounds T, the rows per request (at most 16383)
  *   max_out_beams   bounds every beam width and the final beam F
  *   max_out_tokens  bounds F * T per request
  *   max_inter_beams bounds the hypotheses kept in history per request */

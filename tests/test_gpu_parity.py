@@ -609,6 +609,79 @@ def test_stress_long_keys_tight_thresholds(ft, po, early):
         assert any(len(s) for s in got[0]), "every stress request came back empty"
 
 
+@pytest.mark.parametrize("K,mode", [(8192, "default"), (4097, "default"),
+                                    (20000, "default"), (8192, "search"),
+                                    (8192, "scan"), (8192, "shared")])
+def test_rows_longer_than_lds(ft, po, monkeypatch, K, mode):
+    # K above the 4096 proposals the LDS row holds: the row is searched where
+    # it is staged.  A 32k-token vocabulary, so the wide root takes K hashed
+    # lookups; "search" sends every parent to the binary search, "scan" scans
+    # every child, "shared" spreads every step over 7 workgroups.  Streamed
+    # batches with shuffled rows (staged caller indices), logps rounded to
+    # halves (ties cut by arrival order) and early exit; then the staged path.
+    if mode == "search":
+        monkeypatch.setenv("FT_SCAN_MULT", "0")
+        monkeypatch.setenv("FT_WIDE_MIN", "0")
+    elif mode == "scan":
+        monkeypatch.setenv("FT_SCAN_MULT", "999999")
+    elif mode == "shared":
+        monkeypatch.setenv("FT_WGS", "7")
+        monkeypatch.setenv("FT_SHARE_MIN", "0")
+    V, T, B = 32768, 5, 48
+    toks, offs = ft.synth_keys(150000, V, 3, 7, 1.1, 21)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=K, steps=T, beams=B,
+                  inter=4096)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 8, V, T, K, B, 0.3, 2.0, True, 21, model=1)
+    lp = np.round(lp * 2.0) / 2.0
+    rng = np.random.default_rng(K)
+    for r in range(0, 8, 3):
+        perm = np.stack([rng.permutation(K) for _ in range(T)])
+        ids[r] = np.take_along_axis(ids[r], perm, 1)
+        lp[r] = np.take_along_axis(lp[r], perm, 1)
+    beams = [B] * (T - 1) + [12]
+    for b0 in (0, 4):
+        early = b0 == 4
+        print("long rows", K, mode, "batch", b0, flush=True)
+        got = ft.bs_tbs_gpu(t, 4, [beams] * 4, ids[b0:b0 + 4], lp[b0:b0 + 4],
+                            -10.0, -40.0, 5.0, early)
+        for i in range(4):
+            want = o.tbs(beams, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, early)
+            assert_same_results((got[0][i], got[1][i]), want,
+                                f"K {K} {mode} req {b0 + i} early={early}")
+        assert any(len(x) for x in got[0])
+    ft.stage(t, np.full((4, T), B, np.uint32), ids[:4], lp[:4], -10.0, -40.0, 5.0, False)
+    ft.launch(t)
+    count, norms, lens, tk, _ = ft.fetch(t)
+    for i in range(4):
+        want = o.tbs([B] * T, ids[i], lp[i], -10.0, -40.0, 5.0, False)
+        n = int(count[i])
+        assert_same_results(([tk[i, j, :lens[i, j]].tolist() for j in range(n)],
+                             norms[i, :n]), want, f"K {K} {mode} staged {i}")
+
+
+def test_louds_child_index_is_switched_off(ft, monkeypatch):
+    monkeypatch.setenv("FT_CHILD_INDEX", "louds")
+    t = ft.Trie()
+    t.build([[1, 2], [3]])
+    with pytest.raises(RuntimeError, match="switched off"):
+        t.init_tbs_gpu(1, max_num_topk=4, max_num_outpos=2, max_num_out_beams=2,
+                       max_num_out_tokens=4, max_num_inter_beams=8)
+
+
+def test_topk_limit(ft):
+    t = ft.Trie()
+    t.build([[1], [2]])
+    t.init_tbs_gpu(1, max_num_topk=65535, max_num_outpos=2, max_num_out_beams=2,
+                   max_num_out_tokens=4, max_num_inter_beams=8)
+    with pytest.raises(RuntimeError, match="65535"):
+        t.init_tbs_gpu(1, max_num_topk=65536, max_num_outpos=2, max_num_out_beams=2,
+                       max_num_out_tokens=4, max_num_inter_beams=8)
+
+
+@pytest.mark.skip(reason="the LOUDS child-index kernel faulted the GPU once (tiny tries, "
+                         "after the long-row tests) and the cause is not found; "
+                         "FT_CHILD_INDEX=louds is switched off until it is")
 def test_louds_child_index(ft, po, monkeypatch):
     # child ranges from the LOUDS rank/select directory (FT_CHILD_INDEX=louds)
     # instead of the node records: tiny random tries, a 50k-key trie in
