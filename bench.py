@@ -367,7 +367,8 @@ def run_workload(ft, cfg, args, headline):
         os.environ["FT_CHILD_INDEX"] = "louds"
     free0 = device_free_bytes()
     t0 = time.time()
-    trie.init_tbs_gpu(max(batches), max_num_topk=K, max_num_outpos=T,
+    # (at least 3: an untimed 3-request launch separates the runs of a trace)
+    trie.init_tbs_gpu(max(max(batches), 3), max_num_topk=K, max_num_outpos=T,
                       max_num_out_beams=B, max_num_out_tokens=B * T,
                       max_num_inter_beams=B * T)
     free1 = device_free_bytes()

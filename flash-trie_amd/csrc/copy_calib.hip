@@ -1,16 +1,33 @@
-// copy_calib.hip -- a plain device-to-device copy of known size.
+// copy_calib.hip -- calibration kernels for the search kernel's models.
 //
-// Reference point for the HBM counters: under rocprofv3 --pmc, FETCH_SIZE
-// and WRITE_SIZE of `ftcal::copy_kernel` are compared with the bytes it is
-// known to move (N read, N written per launch), which gives the scale factor
-// applied to the same counters of the search kernel.  Also prints the copy
-// bandwidth it reaches (HIP events).
+// copy: a plain device-to-device copy of known size.  Reference point for
+// the HBM counters: under rocprofv3 --pmc, FETCH_SIZE and WRITE_SIZE of
+// `ftcal::copy_kernel` are compared with the bytes it is known to move (N
+// read, N written per launch), which gives the scale factor applied to the
+// same counters of the search kernel.  Also prints the copy bandwidth it
+// reaches (HIP events).
+//
+// chase: the latency of one dependent global load.  One lane follows a
+// pseudo-random full-period permutation of the 64-byte lines of a buffer
+// (line i holds the index of the next line, (a * i + c) mod lines, a full
+// cycle for a = 1 mod 4, c odd and a power-of-two line count), so every
+// load's address is the previous load's value; plain loads and the
+// device-coherent (agent-scope) loads the search kernel uses for shared
+// data, over buffers from L2-resident to image-sized.
+//
+// pingpong: the latency of a device-coherent store seen by a workgroup on
+// another CU (the post / claim / done handshake of a shared step): two
+// workgroups pass a counter back and forth through two words, every wait
+// bounded.
 //
 // Usage: ft_copy_calib [MiB per buffer, default 1024] [launches, default 5]
+//        ft_copy_calib chase MiB [loads, default 200000]
+//        ft_copy_calib pingpong [rounds, default 20000]
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 
 namespace ftcal {
 
@@ -28,6 +45,64 @@ __global__ void __launch_bounds__(256) fill_kernel(uint4* __restrict__ dst, size
     dst[i] = make_uint4((uint32_t)i, 1u, 2u, 3u);
 }
 
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr uint64_t kLcgA = 0x5851F42D4C957F2Dull;  // = 1 mod 4
+constexpr uint64_t kLcgC = 0x14057B7EF767814Full;  // odd
+
+// line i of `lines` (a power of two) holds the next line's index
+__global__ void __launch_bounds__(256) chase_init(uint32_t* buf, uint64_t lines) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < lines; i += stride)
+    buf[i * 16] = (uint32_t)((kLcgA * i + kLcgC) & (lines - 1));
+}
+
+// one lane: `loads` plain then `loads` device-coherent dependent loads,
+// from line out[2] on; out = {ticks plain, ticks coherent, the next line}
+// (a call continues the cycle where the last one stopped: lines it has not
+// touched, when the buffer holds more than the loads of all calls)
+__global__ void chase_kernel(const uint32_t* buf, uint64_t loads, uint64_t* out) {
+  if (threadIdx.x != 0) return;
+  uint32_t idx = (uint32_t)out[2];
+  const uint64_t t0 = wall_clock64();
+  for (uint64_t s = 0; s < loads; ++s) idx = buf[(uint64_t)idx * 16];
+  const uint64_t t1 = wall_clock64();
+  for (uint64_t s = 0; s < loads; ++s) idx = ld_agent(buf + (uint64_t)idx * 16);
+  const uint64_t t2 = wall_clock64();
+  out[0] = t1 - t0;
+  out[1] = t2 - t1;
+  out[2] = idx;
+}
+
+// blocks 0 and `peer` (one lane each) pass a counter: block 0 writes r to
+// w[0] and waits for w[32] == r, the peer waits for w[0] == r and writes r
+// to w[32]; every wait gives up after `limit` ticks.  out = {ticks, rounds
+// completed}.
+__global__ void pingpong_kernel(uint32_t* w, uint32_t rounds, uint32_t peer, uint64_t limit,
+                                uint64_t* out) {
+  if (threadIdx.x != 0 || (blockIdx.x != 0 && blockIdx.x != peer)) return;
+  const bool lead = blockIdx.x == 0;
+  const uint64_t t0 = wall_clock64();
+  uint32_t r = 1;
+  for (; r <= rounds; ++r) {
+    if (lead) st_agent(w, r);
+    const uint32_t* wait_on = lead ? w + 32 : w;
+    const uint64_t s0 = wall_clock64();
+    while (ld_agent(wait_on) != r && wall_clock64() - s0 < limit) __builtin_amdgcn_s_sleep(0);
+    if (ld_agent(wait_on) != r) break;
+    if (!lead) st_agent(w + 32, r);
+  }
+  if (lead) {
+    out[0] = wall_clock64() - t0;
+    out[1] = r - 1;
+  }
+}
+
 }  // namespace ftcal
 
 #define CHECK(x)                                                              \
@@ -39,7 +114,80 @@ __global__ void __launch_bounds__(256) fill_kernel(uint4* __restrict__ dst, size
     }                                                                         \
   } while (0)
 
+static int wall_khz() {
+  int khz = 0;
+  (void)hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0);
+  return khz > 0 ? khz : 100000;
+}
+
+static int run_chase(size_t mib, uint64_t loads) {
+  if (mib == 0 || (mib & (mib - 1)) || mib > (64u << 10) || loads == 0 || loads > 10000000) {
+    std::fprintf(stderr, "usage: ft_copy_calib chase MiB(power of two, <= 65536) [loads]\n");
+    return 2;
+  }
+  const uint64_t bytes = (uint64_t)mib << 20, lines = bytes / 64;
+  uint32_t* buf = nullptr;
+  uint64_t* out = nullptr;
+  CHECK(hipMalloc(&buf, bytes));
+  CHECK(hipMalloc(&out, 3 * sizeof(uint64_t)));
+  CHECK(hipMemset(out, 0, 3 * sizeof(uint64_t)));
+  ftcal::chase_init<<<256 * 8, 256>>>(buf, lines);
+  CHECK(hipGetLastError());
+  CHECK(hipDeviceSynchronize());
+  uint64_t h[3] = {0, 0, 0};
+  // the first call warms the code path; the second goes on along the cycle
+  // (lines not touched yet unless the buffer holds fewer than 4 x loads)
+  for (int pass = 0; pass < 2; ++pass) {
+    ftcal::chase_kernel<<<1, 64>>>(buf, loads, out);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    CHECK(hipMemcpy(h, out, sizeof(h), hipMemcpyDeviceToHost));
+  }
+  const double ns_tick = 1e6 / wall_khz();
+  std::printf("chase %zu MiB (%llu lines), %llu dependent loads%s: plain %.1f ns, "
+              "device-coherent %.1f ns per load\n",
+              mib, (unsigned long long)lines, (unsigned long long)loads,
+              lines >= 4 * loads ? " on lines not touched before" : " (revisiting lines)",
+              h[0] * ns_tick / loads, h[1] * ns_tick / loads);
+  CHECK(hipFree(buf));
+  CHECK(hipFree(out));
+  return 0;
+}
+
+static int run_pingpong(uint32_t rounds) {
+  if (rounds == 0 || rounds > 1000000) {
+    std::fprintf(stderr, "usage: ft_copy_calib pingpong [rounds <= 1000000]\n");
+    return 2;
+  }
+  uint32_t* w = nullptr;
+  uint64_t* out = nullptr;
+  CHECK(hipMalloc(&w, 256));
+  CHECK(hipMalloc(&out, 2 * sizeof(uint64_t)));
+  const double ns_tick = 1e6 / wall_khz();
+  // the dispatcher deals blocks to the 8 XCDs in turn: block 8 shares block
+  // 0's XCD, block 1 is on the next one
+  for (uint32_t peer : {8u, 1u}) {
+    CHECK(hipMemset(w, 0, 256));
+    ftcal::pingpong_kernel<<<16, 64>>>(w, rounds, peer, 10000000ull, out);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    uint64_t h[2] = {0, 0};
+    CHECK(hipMemcpy(h, out, sizeof(h), hipMemcpyDeviceToHost));
+    std::printf("pingpong with block %u (%s XCD): %llu of %u rounds, %.1f ns one way\n", peer,
+                peer == 8 ? "same" : "another", (unsigned long long)h[1], rounds,
+                h[1] ? h[0] * ns_tick / (2.0 * h[1]) : 0.0);
+  }
+  CHECK(hipFree(w));
+  CHECK(hipFree(out));
+  return 0;
+}
+
 int main(int argc, char** argv) {
+  if (argc > 1 && std::strcmp(argv[1], "chase") == 0)
+    return run_chase(argc > 2 ? std::strtoull(argv[2], nullptr, 10) : 0,
+                     argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 200000);
+  if (argc > 1 && std::strcmp(argv[1], "pingpong") == 0)
+    return run_pingpong(argc > 2 ? (uint32_t)std::strtoul(argv[2], nullptr, 10) : 20000);
   const size_t mib = argc > 1 ? std::strtoull(argv[1], nullptr, 10) : 1024;
   const int launches = argc > 2 ? std::atoi(argv[2]) : 5;
   if (mib == 0 || mib > 16384 || launches < 1 || launches > 1000) {
