@@ -1003,10 +1003,14 @@ __device__ __forceinline__ int grow_find(const uint32_t* rid, uint32_t K, uint32
 // Expands the step's work items: each is (parent, child) for a scanned
 // parent, (parent, proposal) for a searched or hashed parent, or the single
 // pending token of a link parent.  Items go out in chunks of 64 (one per
-// lane of a wave); chunk c belongs to wave c mod nwaves of the request's
-// nwaves waves, so every wave gets an even share of every region of the
-// item space (hashed parents cost a random read per item, scanned ones a
-// coalesced one).  This workgroup's waves are gwave0 .. gwave0 + kWaves - 1.
+// lane of a wave), dealt to the step's workgroups first: chunk c goes to
+// workgroup slice c mod nwg (nwg = nwaves / kWaves) and to its wave
+// (c / nwg) mod kWaves.  So a step of few chunks is spread over as many
+// CUs as it has chunks -- a CU issues the scattered reads of its items at a
+// bounded rate, which sets the time of a step far more than the latency
+// of one read does -- and every wave still gets an even share of every
+// region of the item space (hashed parents cost a random read per item,
+// scanned ones a coalesced one).  This workgroup is slice gwave0 / kWaves.
 // With at most kBlock parents the parent table is read from LDS, where the
 // caller has put it (the leader in its parent phase, a helper with the row);
 // the caller has also zeroed this workgroup's push counters and
@@ -1024,7 +1028,8 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
   uint32_t my_children = 0, my_probes = 0;
   const uint32_t K = v.K, t = v.t;
   const uint32_t nchunks = (W + 63u) >> 6;
-  for (uint32_t c = gwave0 + (tid >> 6); c < nchunks; c += nwaves) {
+  const uint32_t nwg = nwaves / (uint32_t)kWaves, slice = gwave0 / (uint32_t)kWaves;
+  for (uint32_t c = slice + nwg * (tid >> 6); c < nchunks; c += nwaves) {
     const uint32_t w = (c << 6) + lane;
     bool do_next = false, do_sel = false;
     uint32_t cnode = 0, pj = 0, k = 0, tok = 0;
