@@ -15,6 +15,16 @@
 // device-coherent (agent-scope) loads the search kernel uses for shared
 // data, over buffers from L2-resident to image-sized.
 //
+// gather: the rate of independent random loads a CU sustains.  Every lane
+// of `blocks` workgroups of 1024 threads loads 8 lines at a time, each at a
+// pseudo-random line of the buffer (independent addresses: up to the
+// hardware's limit in flight), `rounds` times; over a buffer that the
+// address translation covers and over an image-sized one; 4 bytes a lane,
+// a whole 64-byte line a lane in four 16-byte loads (a cuckoo bucket read
+// by one lane), or a line per four lanes.  Time per load
+// and per workgroup, and the loads in flight that it implies at the chase
+// latency of the same buffer size.
+//
 // pingpong: the latency of a device-coherent store seen by a workgroup on
 // another CU (the post / claim / done handshake of a shared step): two
 // workgroups pass a counter back and forth through two words, every wait
@@ -22,12 +32,16 @@
 //
 // Usage: ft_copy_calib [MiB per buffer, default 1024] [launches, default 5]
 //        ft_copy_calib chase MiB [loads, default 200000]
+//        ft_copy_calib gather MiB [blocks, default 1] [rounds, default 64]
+//                      [0: 4 bytes a lane | 1: 64 bytes a lane | 2: 64 a quad]
 //        ft_copy_calib pingpong [rounds, default 20000]
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
+#include <vector>
 
 namespace ftcal {
 
@@ -77,6 +91,48 @@ __global__ void chase_kernel(const uint32_t* buf, uint64_t loads, uint64_t* out)
   out[0] = t1 - t0;
   out[1] = t2 - t1;
   out[2] = idx;
+}
+
+// gather: lane l of block b, round r, load u reads line
+// mix(((b * 1024 + l) * rounds + r) * 8 + u) of `lines` (a power of two):
+// its first 4 bytes, or (kWhole) all 64 as four 16-byte loads, or
+// (kQuad) the 16 bytes of lane l % 4 of the line of lane l - l % 4 (four
+// lanes read one line together); out[b] = the block's ticks
+template <int kMode>
+__global__ void __launch_bounds__(1024) gather_kernel(const uint32_t* buf, uint64_t lines,
+                                                      uint32_t rounds, uint64_t* out) {
+  const uint64_t gl = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t gq = kMode == 2 ? (gl & ~3ull) : gl;
+  uint32_t acc = 0;
+  __syncthreads();
+  const uint64_t t0 = wall_clock64();
+  for (uint32_t r = 0; r < rounds; ++r) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint64_t x = ((gq * rounds + r) * 8 + (uint64_t)u) * kLcgA + kLcgC;
+      x ^= x >> 29;
+      x *= 0xBF58476D1CE4E5B9ull;
+      x ^= x >> 32;
+      const uint32_t* line = buf + (x & (lines - 1)) * 16;
+      if constexpr (kMode == 0) {
+        v[u] = line[0];
+      } else if constexpr (kMode == 1) {
+        const uint4* q = (const uint4*)line;
+        const uint4 a = q[0], b = q[1], c = q[2], d = q[3];
+        v[u] = a.x + b.y + c.z + d.w;
+      } else {
+        const uint4 a = ((const uint4*)line)[gl & 3];
+        v[u] = a.x + a.y + a.z + a.w;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  __syncthreads();
+  const uint64_t t1 = wall_clock64();
+  if (threadIdx.x == 0) out[blockIdx.x] = t1 - t0;
+  if (acc == 0x9E3779B9u) out[gridDim.x] = acc;  // keeps the loads
 }
 
 // blocks 0 and `peer` (one lane each) pass a counter: block 0 writes r to
@@ -154,6 +210,49 @@ static int run_chase(size_t mib, uint64_t loads) {
   return 0;
 }
 
+static int run_gather(size_t mib, uint32_t blocks, uint32_t rounds, int mode) {
+  if (mode < 0 || mode > 2 || mib == 0 || (mib & (mib - 1)) || mib > (64u << 10) || blocks == 0 || blocks > 4096 ||
+      rounds == 0 || rounds > 4096) {
+    std::fprintf(stderr, "usage: ft_copy_calib gather MiB(power of two, <= 65536) "
+                         "[blocks <= 4096] [rounds <= 4096]\n");
+    return 2;
+  }
+  const uint64_t bytes = (uint64_t)mib << 20, lines = bytes / 64;
+  uint32_t* buf = nullptr;
+  uint64_t* out = nullptr;
+  CHECK(hipMalloc(&buf, bytes));
+  CHECK(hipMalloc(&out, (blocks + 1) * sizeof(uint64_t)));
+  ftcal::chase_init<<<256 * 8, 256>>>(buf, lines);
+  CHECK(hipGetLastError());
+  CHECK(hipDeviceSynchronize());
+  const double ns_tick = 1e6 / wall_khz();
+  std::vector<uint64_t> h(blocks + 1);
+  for (int pass = 0; pass < 2; ++pass) {
+    if (mode == 0) ftcal::gather_kernel<0><<<blocks, 1024>>>(buf, lines, rounds, out);
+    else if (mode == 1) ftcal::gather_kernel<1><<<blocks, 1024>>>(buf, lines, rounds, out);
+    else ftcal::gather_kernel<2><<<blocks, 1024>>>(buf, lines, rounds, out);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    CHECK(hipMemcpy(h.data(), out, (blocks + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  }
+  uint64_t mx = 0, sum = 0;
+  for (uint32_t b = 0; b < blocks; ++b) {
+    mx = std::max(mx, h[b]);
+    sum += h[b];
+  }
+  const double per_wg = 1024.0 * 8 * rounds;
+  static const char* kHow[3] = {"4 bytes a lane", "64 bytes a lane as 4 x 16",
+                                "64 bytes per 4 lanes, 16 each"};
+  std::printf("gather (%s) %zu MiB, %u workgroup(s) x 1024 lanes x %u rounds x 8 loads: "
+              "%.2f ns per load per workgroup (mean), %.2f (slowest); %.2f loads per ns "
+              "over the device\n",
+              kHow[mode], mib, blocks, rounds, sum * ns_tick / blocks / per_wg, mx * ns_tick / per_wg,
+              per_wg * blocks / (mx * ns_tick));
+  CHECK(hipFree(buf));
+  CHECK(hipFree(out));
+  return 0;
+}
+
 static int run_pingpong(uint32_t rounds) {
   if (rounds == 0 || rounds > 1000000) {
     std::fprintf(stderr, "usage: ft_copy_calib pingpong [rounds <= 1000000]\n");
@@ -186,6 +285,11 @@ int main(int argc, char** argv) {
   if (argc > 1 && std::strcmp(argv[1], "chase") == 0)
     return run_chase(argc > 2 ? std::strtoull(argv[2], nullptr, 10) : 0,
                      argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 200000);
+  if (argc > 1 && std::strcmp(argv[1], "gather") == 0)
+    return run_gather(argc > 2 ? std::strtoull(argv[2], nullptr, 10) : 0,
+                      argc > 3 ? (uint32_t)std::strtoul(argv[3], nullptr, 10) : 1u,
+                      argc > 4 ? (uint32_t)std::strtoul(argv[4], nullptr, 10) : 64u,
+                      argc > 5 ? std::atoi(argv[5]) : 0);
   if (argc > 1 && std::strcmp(argv[1], "pingpong") == 0)
     return run_pingpong(argc > 2 ? (uint32_t)std::strtoul(argv[2], nullptr, 10) : 20000);
   const size_t mib = argc > 1 ? std::strtoull(argv[1], nullptr, 10) : 1024;

@@ -183,6 +183,7 @@ __device__ __forceinline__ uint32_t count_before(const uint64_t* rk_key,
   // m is a multiple of 2 * P; entries past the real ones are kRankPad keys
   uint32_t c = 0;
   for (uint32_t q = 0; q < m; q += 2 * P) {
+    asm volatile("" : "+v"(k), "+v"(n));
     ulonglong2 v[P];
     uint4 nd[P / 2];
 #pragma unroll
@@ -258,6 +259,26 @@ __device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
 template <int Ctrl>
 __device__ __forceinline__ uint32_t dpp_move(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, Ctrl, 0xf, 0xf, false);
+}
+template <int Ctrl>
+__device__ __forceinline__ uint64_t dpp_move64(uint64_t x) {
+  return ((uint64_t)dpp_move<Ctrl>((uint32_t)(x >> 32)) << 32) | dpp_move<Ctrl>((uint32_t)x);
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t x, int lane) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+}
+// min (or max) of v over each 16-lane row, in every lane of the row:
+// rotations by 8, 4, 2, 1
+__device__ __forceinline__ uint64_t row_reduce64(uint64_t v, bool take_min) {
+  uint64_t y = dpp_move64<0x128>(v);  // row_ror:8
+  v = take_min ? min(v, y) : max(v, y);
+  y = dpp_move64<0x124>(v);           // row_ror:4
+  v = take_min ? min(v, y) : max(v, y);
+  y = dpp_move64<0x122>(v);           // row_ror:2
+  v = take_min ? min(v, y) : max(v, y);
+  y = dpp_move64<0x121>(v);           // row_ror:1
+  return take_min ? min(v, y) : max(v, y);
 }
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   const uint32_t lane = lane_id(), rl = lane & 15u;
@@ -427,22 +448,23 @@ __device__ __forceinline__ uint64_t kth_u64(uint32_t n, uint32_t need, GetKey gk
         mx = max(mx, k);
       }
     });
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      mn = min(mn, (uint64_t)__shfl_xor((unsigned long long)mn, o, 64));
-      mx = max(mx, (uint64_t)__shfl_xor((unsigned long long)mx, o, 64));
-    }
+    mn = row_reduce64(mn, true);
+    mx = row_reduce64(mx, false);
+    mn = min(min(readlane64(mn, 0), readlane64(mn, 16)),
+             min(readlane64(mn, 32), readlane64(mn, 48)));
+    mx = max(max(readlane64(mx, 0), readlane64(mx, 16)),
+             max(readlane64(mx, 32), readlane64(mx, 48)));
     if (lane == 0) {
       sm.red64[wave] = mn;
       sm.red64[kWaves + wave] = mx;
     }
     __syncthreads();
-    mn = sm.red64[0];
-    mx = sm.red64[kWaves];
-    for (int w = 1; w < kWaves; ++w) {
-      mn = min(mn, sm.red64[w]);
-      mx = max(mx, sm.red64[kWaves + w]);
-    }
+    // every wave combines the partials in one read: lanes 0..15 hold the
+    // waves' minima, lanes 16..31 their maxima
+    static_assert(kWaves == 16, "one DPP row per partial set");
+    const uint64_t v = row_reduce64(sm.red64[lane & 31u], lane < 16u);
+    mn = readlane64(v, 0);
+    mx = readlane64(v, 16);
     __syncthreads();
   }
   if (mn == mx) {
@@ -2834,7 +2856,58 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   if (status == 0) {
     uint64_t* rk_key = (uint64_t*)sm.row_id;
     uint32_t* rk_node = (uint32_t*)sm.row_lp;
-    for (uint32_t jb = 0; jb < nS; jb += kBlock) {
+    // result j, of rank cntless among the selected, into output row cntless
+    auto put = [&](const SelRec& me, uint32_t cntless) {
+      if (cntless >= F) return;
+      onorm[cntless] = me.s * lnf[me.depth];
+      olen[cntless] = me.depth;
+      uint32_t* row = otok + (uint64_t)cntless * d.out_T;
+      if (me.depth >= 1 && me.depth <= d.out_T) {
+        row[me.depth - 1] = me.tok;
+        // each record holds its token and its parent's: two per load
+        uint32_t h = me.phist;
+        for (int pos = (int)me.depth - 2; pos >= 0; pos -= 2) {
+          if (h >= hist_cap) break;
+          const HistRec hr = hist[h];
+          row[pos] = hr.tok;
+          if (pos >= 1) row[pos - 1] = hr.ptok;
+          h = hr.phist2;
+        }
+      }
+    };
+    if (nS > 0 && nS <= (uint32_t)kBlock / 2) {
+      // few results: 2^ls (2..16) neighbouring lanes rank each one, each
+      // over its own slice of `per` entries, and add their counts up
+      uint32_t ls = 1;
+      while (ls < 4 && (nS << (ls + 1)) <= (uint32_t)kBlock) ++ls;
+      const uint32_t j = tid >> ls, sub = tid & ((1u << ls) - 1u);
+      const uint32_t per = (((nS + (1u << ls) - 1u) >> ls) + 15u) & ~15u;
+      // (per << ls) <= nS + (16 << ls) <= kRankChunk: the slices fit
+      uint64_t myk = 0;
+      uint32_t myn = 0, cntless = 0;
+      SelRec me;
+      if (j < nS) {
+        me = selA[j];
+        myk = norm_key(me.s * lnf[me.depth]);
+        myn = me.node;
+      }
+      __syncthreads();
+      if (tid < (per << ls)) {
+        if (tid < nS) {
+          const SelRec o = selA[tid];
+          rk_key[tid] = norm_key(o.s * lnf[o.depth]);
+          rk_node[tid] = o.node;
+        } else {
+          rk_key[tid] = kRankPad;
+          rk_node[tid] = 0;
+        }
+      }
+      __syncthreads();
+      if (j < nS) cntless = count_before<8>(rk_key + sub * per, rk_node + sub * per, per, myk, myn);
+      for (uint32_t o = 1; o < (1u << ls); o <<= 1) cntless += __shfl_xor(cntless, o, 64);
+      if (j < nS && sub == 0) put(me, cntless);
+    }
+    for (uint32_t jb = 0; nS > (uint32_t)kBlock / 2 && jb < nS; jb += kBlock) {
       const uint32_t j = jb + tid;
       uint64_t myk = 0;
       uint32_t myn = 0, cntless = 0;
@@ -2864,23 +2937,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         const uint32_t m = (min((uint32_t)kRankChunk, nS - ib) + 15u) & ~15u;
         if (j < nS) cntless += count_before<8>(rk_key, rk_node, m, myk, myn);
       }
-      if (j < nS && cntless < F) {
-        onorm[cntless] = me.s * lnf[me.depth];
-        olen[cntless] = me.depth;
-        uint32_t* row = otok + (uint64_t)cntless * d.out_T;
-        if (me.depth >= 1 && me.depth <= d.out_T) {
-          row[me.depth - 1] = me.tok;
-          // each record holds its token and its parent's: two per load
-          uint32_t h = me.phist;
-          for (int pos = (int)me.depth - 2; pos >= 0; pos -= 2) {
-            if (h >= hist_cap) break;
-            const HistRec hr = hist[h];
-            row[pos] = hr.tok;
-            if (pos >= 1) row[pos - 1] = hr.ptok;
-            h = hr.phist2;
-          }
-        }
-      }
+      if (j < nS) put(me, cntless);
     }
   }
   __syncthreads();
