@@ -246,9 +246,27 @@ def harness_sweep(ft, trie, beams, ids, lp, batches, rules, passes, lists, what)
                   "mean_ms": float(np.mean([c.mean() for c in calls])),
                   "p99_ms": float(np.mean([np.percentile(c, 99) for c in calls])),
                   "calls_per_pass": n // b}
+        if lists:
+            # the caller's own share of a call: the three .tolist() and the
+            # release of the lists, with no search -- the wall this harness
+            # cannot go below on this host
+            fw = []
+            for p in range(1 + passes):
+                t0 = time.perf_counter()
+                for b0 in range(0, n, b):
+                    x = (beams[b0:b0 + b].tolist(), ids[b0:b0 + b].tolist(),
+                         lp[b0:b0 + b].tolist())
+                    del x
+                if p >= 1:
+                    fw.append(time.perf_counter() - t0)
+            out[b]["caller_ms"] = float(np.mean(fw)) / (n // b) * 1e3
+            out[b]["caller_only_qps"] = float(n / np.mean(fw))
+            out[b]["search_ms"] = out[b]["mean_ms"] - out[b]["caller_ms"]
         log(f"{what} batch {b}: {out[b]['qps']:.0f} q/s harness wall "
             f"({'lists' if lists else 'numpy'}; passes {out[b]['qps_passes']}), "
-            f"mean {out[b]['mean_ms']:.3f} ms p99 {out[b]['p99_ms']:.3f} ms per call")
+            f"mean {out[b]['mean_ms']:.3f} ms p99 {out[b]['p99_ms']:.3f} ms per call"
+            + (f"; the lists alone {out[b]['caller_ms']:.3f} ms a call "
+               f"({out[b]['caller_only_qps']:.0f} q/s with no search)" if lists else ""))
     return out
 
 

@@ -423,6 +423,28 @@ PYBIND11_MODULE(flashtrie, m) {
       },
       py::arg("beams"), py::arg("topk_id"), py::arg("topk_logp"), py::arg("generic") = false);
 
+  // result_lists on caller-made results (tests): lengths[n], tokens[n, T]
+  m.def(
+      "_result_lists",
+      [](py::array_t<uint32_t, py::array::c_style | py::array::forcecast> lengths,
+         py::array_t<uint32_t, py::array::c_style | py::array::forcecast> tokens,
+         py::array_t<double, py::array::c_style | py::array::forcecast> norms) {
+        if (tokens.ndim() != 2 || lengths.ndim() != 1 || norms.ndim() != 1 ||
+            lengths.shape(0) != tokens.shape(0) || norms.shape(0) != tokens.shape(0))
+          throw py::value_error("_result_lists: lengths[n], tokens[n, T], norms[n]");
+        ft_result r{};
+        r.capacity = r.count = (uint32_t)tokens.shape(0);
+        r.token_stride = (uint32_t)tokens.shape(1);
+        for (py::ssize_t j = 0; j < lengths.shape(0); ++j)
+          if (lengths.data()[j] > r.token_stride) throw py::value_error("_result_lists: length");
+        r.length = const_cast<uint32_t*>(lengths.data());
+        r.tokens = const_cast<uint32_t*>(tokens.data());
+        r.logp_norm = const_cast<double*>(norms.data());
+        auto sl = ftpy::result_lists(r);
+        return py::make_tuple(sl.first, sl.second);
+      },
+      py::arg("lengths"), py::arg("tokens"), py::arg("norms"));
+
   m.def("load_topk_keys_and_scores", &marisa::load_topk_keys_and_scores,
         py::arg("dataset_dir"));
 

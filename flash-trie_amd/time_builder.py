@@ -1,0 +1,66 @@
+"""Times the key-set builder (Trie.build_arrays: explicit keys -> trie
+image, the work of louds-trie.cc:397-640) on N synthetic unique keys over
+the paper trie's vocabulary (2.2M tokens, Zipf(1.05)), uniform length
+3-9 (mean 6, the paper trie's mean key length), and reports wall time and
+peak resident memory of key generation and of the build.
+
+    python time_builder.py N [--vocab V] [--lmax L] [--seed S]
+
+One JSON line: keys, tokens, generate_s, build_s, nodes, image_bytes,
+rss_after_generate_gib, peak_rss_gib (the process's high-water mark after
+the build; the generated keys stay resident during it)."""
+import argparse
+import json
+import os
+import resource
+import sys
+import time
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import flashtrie as ft  # noqa: E402
+
+
+def hwm_gib():
+    # VmHWM: the peak resident set of this process
+    with open("/proc/self/status") as f:
+        for line in f:
+            if line.startswith("VmHWM:"):
+                return int(line.split()[1]) / (1 << 20)
+    return resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / (1 << 20)
+
+
+def rss_gib():
+    with open("/proc/self/status") as f:
+        for line in f:
+            if line.startswith("VmRSS:"):
+                return int(line.split()[1]) / (1 << 20)
+    return 0.0
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("n", type=int)
+    ap.add_argument("--vocab", type=int, default=2_200_000)
+    ap.add_argument("--lmax", type=int, default=9)
+    ap.add_argument("--seed", type=int, default=1)
+    a = ap.parse_args()
+    t0 = time.perf_counter()
+    toks, offs = ft.synth_keys(a.n, a.vocab, 3, a.lmax, 1.05, a.seed)
+    t1 = time.perf_counter()
+    rss_gen = rss_gib()
+    print(f"[time_builder] generated {a.n} keys ({toks.size} tokens) in {t1 - t0:.1f} s",
+          file=sys.stderr, flush=True)
+    t = ft.Trie()
+    t2 = time.perf_counter()
+    t.build_arrays(toks, offs)
+    t3 = time.perf_counter()
+    out = {"keys": a.n, "tokens": int(toks.size), "generate_s": round(t1 - t0, 2),
+           "build_s": round(t3 - t2, 2), "num_keys": int(t.num_keys()),
+           "image_bytes": int(t.image_view().nbytes),
+           "rss_after_generate_gib": round(rss_gen, 2), "peak_rss_gib": round(hwm_gib(), 2),
+           "key_length": [3, a.lmax], "cpus": os.cpu_count()}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -145,3 +145,22 @@ def test_host_search_numpy_equals_lists(ft, po):
                      ([8] * 6, ids[r].astype(np.int64), lp[r].astype(np.float64))]:
             got = ft.tbs(t, *args, -10.0, -40.0, 5.0, False, False)
             assert_same_results(got[:2], want, f"request {r}")
+
+
+def test_result_lists(ft):
+    # the lists bs_tbs_gpu returns: each result's first `length` tokens as
+    # ints (ids up to 2^32 - 1), its norm as a float
+    big = (1 << 32) - 1
+    toks = np.array([[7, 2_000_000, 0], [2_000_000, 7, big], [big, 0, 0]], np.uint32)
+    lens = np.array([2, 3, 1], np.uint32)
+    norms = np.array([-1.5, -2.25, 0.0])
+    sents, ns = ft._result_lists(lens, toks, norms)
+    assert sents == [[7, 2_000_000], [2_000_000, 7, big], [big]]
+    assert ns == [-1.5, -2.25, 0.0]
+    assert all(type(x) is int for s in sents for x in s)
+    assert all(type(x) is float for x in ns)
+    e, en = ft._result_lists(np.zeros(0, np.uint32), np.zeros((0, 3), np.uint32),
+                             np.zeros(0))
+    assert e == [] and en == []
+    with pytest.raises(ValueError):
+        ft._result_lists(np.array([4, 0, 0], np.uint32), toks, norms)
