@@ -729,6 +729,55 @@ PYBIND11_MODULE(flashtrie, m) {
       py::arg("trie"), py::arg("n_keys"), py::arg("vocab"), py::arg("s"),
       py::arg("seed"), py::arg("lmin") = 3, py::arg("lmax") = 16,
       py::arg("p_end") = 0.25, py::arg("threads") = 0, py::arg("unique_keys") = 0);
+  // every key of a trie as (tokens, offsets), in lexicographic order: a
+  // depth-first walk of the image (children in ascending first-token
+  // order), each node's edge from first_tok or tail[]
+  m.def(
+      "keys_of",
+      [](const Trie& trie) {
+        const ftamd::ImageBlob& img = image_of(trie);
+        const ft_node_rec* R = img.recs();
+        const uint32_t* tail = img.tail();
+        const uint64_t N = img.header().num_nodes;
+        uint64_t nk = 0, nt = 0;
+        for (uint64_t n = 0; n < N; ++n)
+          if (R[n].meta & FT_META_TERMINAL) {
+            ++nk;
+            nt += R[n].meta & FT_META_DEPTH_MASK;
+          }
+        py::array_t<uint32_t> toks((py::ssize_t)nt);
+        py::array_t<uint64_t> offs((py::ssize_t)(nk + 1));
+        uint32_t* T = toks.mutable_data();
+        uint64_t* O = offs.mutable_data();
+        {
+          py::gil_scoped_release nogil;
+          std::vector<uint32_t> pre, stack{0u};
+          uint64_t k = 0, o = 0;
+          O[0] = 0;
+          while (!stack.empty()) {
+            const uint32_t n = stack.back();
+            stack.pop_back();
+            const uint32_t meta = R[n].meta;
+            const uint32_t sd = meta & FT_META_DEPTH_MASK;
+            const uint32_t el = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+            if (n != 0) {
+              pre.resize(sd - el);
+              for (uint32_t i = 0; i < el; ++i)
+                pre.push_back((meta & FT_META_LINK) ? tail[(uint64_t)R[n].tail_off + i]
+                                                    : R[n].first_tok);
+            }
+            if (meta & FT_META_TERMINAL) {
+              std::memcpy(T + o, pre.data(), (size_t)sd * 4);
+              o += sd;
+              O[++k] = o;
+            }
+            for (uint32_t c = R[n + 1].child_begin; c > R[n].child_begin; --c)
+              stack.push_back(c - 1);
+          }
+        }
+        return py::make_tuple(toks, offs);
+      },
+      py::arg("trie"));
   m.def(
       "validate_image",
       [](const Trie& trie) {

@@ -5,6 +5,12 @@ the paper trie's vocabulary (2.2M tokens, Zipf(1.05)), uniform length
 peak resident memory of key generation and of the build.
 
     python time_builder.py N [--vocab V] [--lmax L] [--seed S]
+    python time_builder.py N --from-paper
+
+With --from-paper the keys are those of a paper-shape trie of about N
+unique keys (synth_paper_trie, length 3-16 with mean ~6, Zipf(1.05)
+prefix sharing), read back from its image in lexicographic order; the
+build from them must give the same image, which is checked.
 
 One JSON line: keys, tokens, generate_s, build_s, nodes, image_bytes,
 rss_after_generate_gib, peak_rss_gib (the process's high-water mark after
@@ -43,22 +49,37 @@ def main():
     ap.add_argument("--vocab", type=int, default=2_200_000)
     ap.add_argument("--lmax", type=int, default=9)
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--from-paper", action="store_true")
     a = ap.parse_args()
     t0 = time.perf_counter()
-    toks, offs = ft.synth_keys(a.n, a.vocab, 3, a.lmax, 1.05, a.seed)
+    src = None
+    if a.from_paper:
+        # the paper workload's ratio of draws to unique keys (845.45M draws
+        # give 799.49M unique keys)
+        src = ft.Trie()
+        ft.synth_paper_trie(src, int(a.n * 845.45 / 799.49), a.vocab, 1.05, a.seed)
+        toks, offs = ft.keys_of(src)
+    else:
+        toks, offs = ft.synth_keys(a.n, a.vocab, 3, a.lmax, 1.05, a.seed)
     t1 = time.perf_counter()
     rss_gen = rss_gib()
-    print(f"[time_builder] generated {a.n} keys ({toks.size} tokens) in {t1 - t0:.1f} s",
+    print(f"[time_builder] generated {offs.size - 1} keys ({toks.size} tokens) in {t1 - t0:.1f} s",
           file=sys.stderr, flush=True)
     t = ft.Trie()
     t2 = time.perf_counter()
     t.build_arrays(toks, offs)
     t3 = time.perf_counter()
-    out = {"keys": a.n, "tokens": int(toks.size), "generate_s": round(t1 - t0, 2),
+    same = None
+    if src is not None:
+        import numpy as np
+        same = bool(np.array_equal(src.image_view(), t.image_view()))
+    out = {"keys": int(offs.size - 1), "tokens": int(toks.size), "generate_s": round(t1 - t0, 2),
            "build_s": round(t3 - t2, 2), "num_keys": int(t.num_keys()),
            "image_bytes": int(t.image_view().nbytes),
            "rss_after_generate_gib": round(rss_gen, 2), "peak_rss_gib": round(hwm_gib(), 2),
-           "key_length": [3, a.lmax], "cpus": os.cpu_count()}
+           "keys_from": "paper-shape trie" if a.from_paper else "synth_keys",
+           "key_length": [3, 16] if a.from_paper else [3, a.lmax], "cpus": os.cpu_count(),
+           "image_equals_source": same}
     print(json.dumps(out), flush=True)
 
 

@@ -117,3 +117,17 @@ def test_paper_trie_topped_up_to_exact_unique_keys(ft):
     with pytest.raises(RuntimeError, match="more than the target"):
         ft.synth_paper_trie(ft.Trie(), 30000, 5000, 1.05, 7,
                             unique_keys=base.num_keys() - 1)
+
+
+def test_keys_of_round_trip(ft):
+    # keys_of lists every key in lexicographic order; building from them
+    # gives the same image
+    t = ft.Trie()
+    ft.synth_paper_trie(t, 20000, 3000, 1.05, 5)
+    toks, offs = ft.keys_of(t)
+    keys = [tuple(toks[offs[i]:offs[i + 1]]) for i in range(offs.size - 1)]
+    assert len(keys) == t.num_keys()
+    assert keys == sorted(set(tuple(k) for k in _keys_of(t.image())))
+    u = ft.Trie()
+    u.build_arrays(toks, offs)
+    assert np.array_equal(t.image(), u.image())
