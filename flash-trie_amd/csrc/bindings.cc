@@ -729,12 +729,13 @@ PYBIND11_MODULE(flashtrie, m) {
       py::arg("trie"), py::arg("n_keys"), py::arg("vocab"), py::arg("s"),
       py::arg("seed"), py::arg("lmin") = 3, py::arg("lmax") = 16,
       py::arg("p_end") = 0.25, py::arg("threads") = 0, py::arg("unique_keys") = 0);
-  // every key of a trie as (tokens, offsets), in lexicographic order: a
-  // depth-first walk of the image (children in ascending first-token
-  // order), each node's edge from first_tok or tail[]
+  // every key of a trie as (tokens, offsets), in lexicographic order (or,
+  // with a nonzero seed, in a seeded random order): a depth-first walk of
+  // the image (children in ascending first-token order), each node's edge
+  // from first_tok or tail[]
   m.def(
       "keys_of",
-      [](const Trie& trie) {
+      [](const Trie& trie, uint64_t shuffle_seed) {
         const ftamd::ImageBlob& img = image_of(trie);
         const ft_node_rec* R = img.recs();
         const uint32_t* tail = img.tail();
@@ -751,33 +752,59 @@ PYBIND11_MODULE(flashtrie, m) {
         uint64_t* O = offs.mutable_data();
         {
           py::gil_scoped_release nogil;
-          std::vector<uint32_t> pre, stack{0u};
-          uint64_t k = 0, o = 0;
-          O[0] = 0;
-          while (!stack.empty()) {
-            const uint32_t n = stack.back();
-            stack.pop_back();
-            const uint32_t meta = R[n].meta;
-            const uint32_t sd = meta & FT_META_DEPTH_MASK;
-            const uint32_t el = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
-            if (n != 0) {
-              pre.resize(sd - el);
-              for (uint32_t i = 0; i < el; ++i)
-                pre.push_back((meta & FT_META_LINK) ? tail[(uint64_t)R[n].tail_off + i]
-                                                    : R[n].first_tok);
+          // visit(f): f(key index in walk order, its tokens, length)
+          auto walk = [&](auto&& f) {
+            std::vector<uint32_t> pre, stack{0u};
+            uint64_t k = 0;
+            while (!stack.empty()) {
+              const uint32_t n = stack.back();
+              stack.pop_back();
+              const uint32_t meta = R[n].meta;
+              const uint32_t sd = meta & FT_META_DEPTH_MASK;
+              const uint32_t el = (meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+              if (n != 0) {
+                pre.resize(sd - el);
+                for (uint32_t i = 0; i < el; ++i)
+                  pre.push_back((meta & FT_META_LINK) ? tail[(uint64_t)R[n].tail_off + i]
+                                                      : R[n].first_tok);
+              }
+              if (meta & FT_META_TERMINAL) f(k++, pre.data(), sd);
+              for (uint32_t c = R[n + 1].child_begin; c > R[n].child_begin; --c)
+                stack.push_back(c - 1);
             }
-            if (meta & FT_META_TERMINAL) {
-              std::memcpy(T + o, pre.data(), (size_t)sd * 4);
-              o += sd;
-              O[++k] = o;
+          };
+          if (shuffle_seed == 0) {
+            uint64_t o = 0;
+            O[0] = 0;
+            walk([&](uint64_t k, const uint32_t* p, uint32_t len) {
+              std::memcpy(T + o, p, (size_t)len * 4);
+              o += len;
+              O[k + 1] = o;
+            });
+          } else {
+            // slot[k]: where walk key k goes (a seeded Fisher-Yates
+            // permutation); lengths in slot order, then their prefix
+            std::vector<uint64_t> slot(nk);
+            for (uint64_t k = 0; k < nk; ++k) slot[k] = k;
+            uint64_t x = shuffle_seed * 0x9E3779B97F4A7C15ull + 1;
+            for (uint64_t k = nk; k > 1; --k) {
+              x ^= x >> 12;
+              x ^= x << 25;
+              x ^= x >> 27;
+              const uint64_t r = (x * 0x2545F4914F6CDD1Dull) % k;
+              std::swap(slot[k - 1], slot[r]);
             }
-            for (uint32_t c = R[n + 1].child_begin; c > R[n].child_begin; --c)
-              stack.push_back(c - 1);
+            O[0] = 0;
+            walk([&](uint64_t k, const uint32_t*, uint32_t len) { O[slot[k] + 1] = len; });
+            for (uint64_t k = 0; k < nk; ++k) O[k + 1] += O[k];
+            walk([&](uint64_t k, const uint32_t* p, uint32_t len) {
+              std::memcpy(T + O[slot[k]], p, (size_t)len * 4);
+            });
           }
         }
         return py::make_tuple(toks, offs);
       },
-      py::arg("trie"));
+      py::arg("trie"), py::arg("shuffle_seed") = 0);
   m.def(
       "validate_image",
       [](const Trie& trie) {

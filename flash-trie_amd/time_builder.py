@@ -5,12 +5,13 @@ the paper trie's vocabulary (2.2M tokens, Zipf(1.05)), uniform length
 peak resident memory of key generation and of the build.
 
     python time_builder.py N [--vocab V] [--lmax L] [--seed S]
-    python time_builder.py N --from-paper
+    python time_builder.py N --from-paper [--shuffle]
 
 With --from-paper the keys are those of a paper-shape trie of about N
 unique keys (synth_paper_trie, length 3-16 with mean ~6, Zipf(1.05)
-prefix sharing), read back from its image in lexicographic order; the
-build from them must give the same image, which is checked.
+prefix sharing), read back from its image in lexicographic order (with
+--shuffle, in a seeded random order); the build from them must give the
+same image, which is checked.
 
 One JSON line: keys, tokens, generate_s, build_s, nodes, image_bytes,
 rss_after_generate_gib, peak_rss_gib (the process's high-water mark after
@@ -50,6 +51,7 @@ def main():
     ap.add_argument("--lmax", type=int, default=9)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--from-paper", action="store_true")
+    ap.add_argument("--shuffle", action="store_true")
     a = ap.parse_args()
     t0 = time.perf_counter()
     src = None
@@ -58,7 +60,7 @@ def main():
         # give 799.49M unique keys)
         src = ft.Trie()
         ft.synth_paper_trie(src, int(a.n * 845.45 / 799.49), a.vocab, 1.05, a.seed)
-        toks, offs = ft.keys_of(src)
+        toks, offs = ft.keys_of(src, a.seed if a.shuffle else 0)
     else:
         toks, offs = ft.synth_keys(a.n, a.vocab, 3, a.lmax, 1.05, a.seed)
     t1 = time.perf_counter()
@@ -77,7 +79,8 @@ def main():
            "build_s": round(t3 - t2, 2), "num_keys": int(t.num_keys()),
            "image_bytes": int(t.image_view().nbytes),
            "rss_after_generate_gib": round(rss_gen, 2), "peak_rss_gib": round(hwm_gib(), 2),
-           "keys_from": "paper-shape trie" if a.from_paper else "synth_keys",
+           "keys_from": ("paper-shape trie, " + ("shuffled" if a.shuffle else "sorted"))
+           if a.from_paper else "synth_keys",
            "key_length": [3, 16] if a.from_paper else [3, a.lmax], "cpus": os.cpu_count(),
            "image_equals_source": same}
     print(json.dumps(out), flush=True)

@@ -131,3 +131,10 @@ def test_keys_of_round_trip(ft):
     u = ft.Trie()
     u.build_arrays(toks, offs)
     assert np.array_equal(t.image(), u.image())
+    # a seeded random order of the same keys builds the same image
+    st, so = ft.keys_of(t, 7)
+    shuffled = [tuple(st[so[i]:so[i + 1]]) for i in range(so.size - 1)]
+    assert shuffled != keys and sorted(shuffled) == keys
+    w = ft.Trie()
+    w.build_arrays(st, so)
+    assert np.array_equal(t.image(), w.image())
