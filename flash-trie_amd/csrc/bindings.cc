@@ -272,7 +272,8 @@ PYBIND11_MODULE(flashtrie, m) {
       // ---- beyond the reference ----
       .def("build_arrays",
            [](Trie& t, py::array_t<uint32_t, py::array::c_style | py::array::forcecast> toks,
-              py::array_t<uint64_t, py::array::c_style | py::array::forcecast> offs) {
+              py::array_t<uint64_t, py::array::c_style | py::array::forcecast> offs,
+             bool progress) {
              if (offs.ndim() != 1 || offs.shape(0) < 1)
                throw marisa::Exception(MARISA_CODE_ERROR, "offsets must be 1-D, length >= 1");
              const uint64_t n = (uint64_t)offs.shape(0) - 1;
@@ -284,12 +285,12 @@ PYBIND11_MODULE(flashtrie, m) {
              bool ok;
              {
                py::gil_scoped_release nogil;
-               ok = ftamd::build_image_from_keys(toks.data(), o, n, &img, &err);
+               ok = ftamd::build_image_from_keys(toks.data(), o, n, &img, &err, 0, progress);
              }
              if (!ok) throw marisa::Exception(MARISA_SIZE_ERROR, "build: " + err);
              t.assign_image(img.data(), img.size());
            },
-           py::arg("tokens"), py::arg("offsets"))
+           py::arg("tokens"), py::arg("offsets"), py::arg("progress") = false)
       .def("image",
            [](const Trie& t) {
              const ftamd::ImageBlob& img = image_of(t);
@@ -735,7 +736,13 @@ PYBIND11_MODULE(flashtrie, m) {
   // from first_tok or tail[]
   m.def(
       "keys_of",
-      [](const Trie& trie, uint64_t shuffle_seed) {
+      [](const Trie& trie, uint64_t shuffle_seed, bool progress) {
+        auto say = [&](const char* what) {
+          if (progress) {
+            std::fprintf(stderr, "[keys_of] %s\n", what);
+            std::fflush(stderr);
+          }
+        };
         const ftamd::ImageBlob& img = image_of(trie);
         const ft_node_rec* R = img.recs();
         const uint32_t* tail = img.tail();
@@ -794,17 +801,20 @@ PYBIND11_MODULE(flashtrie, m) {
               const uint64_t r = (x * 0x2545F4914F6CDD1Dull) % k;
               std::swap(slot[k - 1], slot[r]);
             }
+            say("order drawn");
             O[0] = 0;
             walk([&](uint64_t k, const uint32_t*, uint32_t len) { O[slot[k] + 1] = len; });
             for (uint64_t k = 0; k < nk; ++k) O[k + 1] += O[k];
+            say("offsets placed");
             walk([&](uint64_t k, const uint32_t* p, uint32_t len) {
               std::memcpy(T + O[slot[k]], p, (size_t)len * 4);
             });
           }
+          say("keys written");
         }
         return py::make_tuple(toks, offs);
       },
-      py::arg("trie"), py::arg("shuffle_seed") = 0);
+      py::arg("trie"), py::arg("shuffle_seed") = 0, py::arg("progress") = false);
   m.def(
       "validate_image",
       [](const Trie& trie) {

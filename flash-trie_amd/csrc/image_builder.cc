@@ -26,6 +26,8 @@
 
 #if defined(_OPENMP)
 #include <parallel/algorithm>
+#include <chrono>
+#include <cstdio>
 #endif
 
 namespace ftamd {
@@ -185,8 +187,16 @@ struct Range {
 
 bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
                            uint64_t nkeys, ImageBlob* out, std::string* err,
-                           int threads) {
+                           int threads, bool progress) {
   (void)threads;
+  const auto t_start = std::chrono::steady_clock::now();
+  auto report = [&](const std::string& what) {
+    if (!progress) return;
+    const double s =
+        std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
+    std::fprintf(stderr, "[build] %s at %.1f s\n", what.c_str(), s);
+    std::fflush(stderr);
+  };
   KeySet ks{toks, offs};
   for (uint64_t i = 0; i < nkeys; ++i) {
     const uint32_t L = ks.len(i);
@@ -202,6 +212,7 @@ bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
       }
     }
   }
+  report("keys validated");
   std::vector<uint64_t> idx(nkeys);
   std::iota(idx.begin(), idx.end(), 0ull);
   auto less = [&](uint64_t a, uint64_t b) {
@@ -218,6 +229,7 @@ bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
 #else
   std::sort(idx.begin(), idx.end(), less);
 #endif
+  report("keys sorted");
   // merge duplicates
   auto same = [&](uint64_t a, uint64_t b) {
     const uint32_t la = ks.len(a);
@@ -226,6 +238,7 @@ bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
   };
   idx.erase(std::unique(idx.begin(), idx.end(), same), idx.end());
   const uint64_t n = idx.size();
+  report("duplicates merged (" + std::to_string(n) + " keys)");
   auto key_len = [&](uint64_t i) { return ks.len(idx[i]); };
   auto key_at = [&](uint64_t i, uint32_t p) { return ks.ptr(idx[i])[p]; };
 
@@ -299,6 +312,7 @@ bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
     }
     level_base += level.size();
     level.swap(next_level);
+    report("level done, " + std::to_string(recs.size()) + " nodes");
   }
   const uint64_t N = recs.size();
   if (!out->allocate(N, tail.size())) {

@@ -82,10 +82,12 @@ bool write_all(int fd, const void* p, size_t n);
 // the reference's node numbering (MARISA BFS, label order, path compression:
 // lib/marisa/grimoire/trie/louds-trie.cc:477-588).  Duplicate keys are
 // merged.  Returns false and sets *err on invalid keys (a token >= 2^31, a
-// key longer than 16383 tokens, or more than 2^32 - 2 nodes).
+// key longer than 16383 tokens, or more than 2^32 - 2 nodes).  With
+// `progress`, each phase's end is reported on stderr with its elapsed
+// time (validation, sort, duplicate merge, every level of the walk).
 bool build_image_from_keys(const uint32_t* toks, const uint64_t* offs,
                            uint64_t nkeys, ImageBlob* out, std::string* err,
-                           int threads = 0);
+                           int threads = 0, bool progress = false);
 
 // Checks the structural invariants of an image (child ranges, depths,
 // parents, tail bounds).  Used on images read from disk.

@@ -60,7 +60,9 @@ def main():
         # give 799.49M unique keys)
         src = ft.Trie()
         ft.synth_paper_trie(src, int(a.n * 845.45 / 799.49), a.vocab, 1.05, a.seed)
-        toks, offs = ft.keys_of(src, a.seed if a.shuffle else 0)
+        print(f"[time_builder] paper-shape trie of {src.num_keys()} keys made", file=sys.stderr,
+              flush=True)
+        toks, offs = ft.keys_of(src, a.seed if a.shuffle else 0, progress=True)
     else:
         toks, offs = ft.synth_keys(a.n, a.vocab, 3, a.lmax, 1.05, a.seed)
     t1 = time.perf_counter()
@@ -69,7 +71,7 @@ def main():
           file=sys.stderr, flush=True)
     t = ft.Trie()
     t2 = time.perf_counter()
-    t.build_arrays(toks, offs)
+    t.build_arrays(toks, offs, progress=True)
     t3 = time.perf_counter()
     same = None
     if src is not None:
