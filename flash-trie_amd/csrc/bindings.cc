@@ -165,6 +165,7 @@ py::tuple gpu_search(Trie& trie, size_t B, const py::object* one_beams,
   }
   const auto end = clk::now();
   if (rc) throw_search(rc);
+  ftpy::GcPause no_gc;
   py::list sents(B), norms(B), phase(B);
   for (size_t i = 0; i < B; ++i) {
     const ft_result& o = b.res[i];
@@ -376,6 +377,7 @@ PYBIND11_MODULE(flashtrie, m) {
           if (q.F) trie.tbs(input);
         }
         auto end = std::chrono::high_resolution_clock::now();
+        ftpy::GcPause no_gc;
         return py::make_tuple(py::cast(out_sent), py::cast(out_logp_norm),
                               marisa::get_msec(start, end));
       },
@@ -441,6 +443,7 @@ PYBIND11_MODULE(flashtrie, m) {
         r.length = const_cast<uint32_t*>(lengths.data());
         r.tokens = const_cast<uint32_t*>(tokens.data());
         r.logp_norm = const_cast<double*>(norms.data());
+        ftpy::GcPause no_gc;
         auto sl = ftpy::result_lists(r);
         return py::make_tuple(sl.first, sl.second);
       },

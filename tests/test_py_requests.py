@@ -164,3 +164,36 @@ def test_result_lists(ft):
     assert e == [] and en == []
     with pytest.raises(ValueError):
         ft._result_lists(np.array([4, 0, 0], np.uint32), toks, norms)
+
+
+def test_result_lists_leave_the_collector_as_found(ft):
+    # the result lists are built with the cyclic collector held off; its
+    # state is restored after, also when the call raises
+    import gc
+    toks = np.arange(12, dtype=np.uint32).reshape(4, 3)
+    lens = np.array([3, 2, 1, 0], np.uint32)
+    norms = np.zeros(4)
+    was = gc.isenabled()
+    try:
+        gc.enable()
+        ft._result_lists(lens, toks, norms)
+        assert gc.isenabled()
+        with pytest.raises(ValueError):
+            ft._result_lists(np.array([9, 0, 0, 0], np.uint32), toks, norms)
+        assert gc.isenabled()
+        gc.disable()
+        ft._result_lists(lens, toks, norms)
+        assert not gc.isenabled()
+    finally:
+        (gc.enable if was else gc.disable)()
+
+
+def test_host_search_leaves_the_collector_as_found(ft):
+    import gc
+    toks, offs = ft.synth_keys(2000, 256, 3, 6, 1.1, 3)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    ids, lp = ft.synth_requests(t, 0, 1, 256, 5, 16, 4, 0.3, 2.0, True, 1)
+    assert gc.isenabled()
+    ft.tbs(t, [4] * 5, ids[0], lp[0], -10.0, -40.0, 5.0, False, False)
+    assert gc.isenabled()
