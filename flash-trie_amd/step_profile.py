@@ -79,7 +79,8 @@ def main():
     import flashtrie as ft
     import workloads as wl
 
-    print(f"library {ft.__file__} build {ft.build_id()}", flush=True)
+    print(f"library {os.path.relpath(ft.__file__, os.path.dirname(HERE))} build "
+          f"{ft.build_id()}", flush=True)
     if a.no_calib:
         L_img, L_l2, L_post = 0.40, 0.09, 0.45
     else:
