@@ -293,7 +293,7 @@ def fnv_results(sents, norms):
 def oracle_of(trie):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
-    return pyoracle, wl.oracle(pyoracle, trie)
+    return pyoracle, pyoracle.OracleTrie.from_trie(trie)
 
 
 def cpu_info():

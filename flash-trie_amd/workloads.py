@@ -73,14 +73,3 @@ def requests(ft, t, name, model, first, n, beam, topk=None):
     else:
         raise ValueError(model)
     return np.full((n, T), beam, dtype=np.uint32), ids, lp
-
-
-def oracle(po, t):
-    """The CPU oracle over the trie's own image (no copy: it keeps views of
-    the image's record and tail arrays)."""
-    img = t.image_view()
-    hdr = np.frombuffer(img[:64].tobytes(), dtype="<u8", count=8)
-    nn, tl, ro, to = int(hdr[1]), int(hdr[3]), int(hdr[4]), int(hdr[6])
-    recs = img[ro:ro + (nn + 1) * 16]
-    tail = img[to:to + max(tl, 1) * 4].view(np.uint32)
-    return po.OracleTrie.from_image(recs, tail, nn)

@@ -98,6 +98,17 @@ class OracleTrie:
         h = lib().ot_wrap_image(_ptr(recs), _ptr(tail), num_nodes)
         return cls(h, keep=(recs, tail))
 
+    @classmethod
+    def from_trie(cls, t):
+        """The oracle over a flashtrie.Trie's own image (no copy: it keeps
+        views of the image's record and tail arrays)."""
+        img = t.image_view()
+        hdr = np.frombuffer(img[:64].tobytes(), dtype="<u8", count=8)
+        nn, tl, ro, to = int(hdr[1]), int(hdr[3]), int(hdr[4]), int(hdr[6])
+        recs = img[ro:ro + (nn + 1) * 16]
+        tail = img[to:to + max(tl, 1) * 4].view(np.uint32)
+        return cls.from_image(recs, tail, nn)
+
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:
             _lib.ot_free(self.h)

@@ -26,7 +26,7 @@ def c2(ft, po):
                                 True, 0, model=0)
     import numpy as np
     beams = np.full((1000, 12), 100, dtype=np.uint32)
-    want = oracle_all(wl.oracle(po, t), beams, ids, lp, wl.RULES["c2"])
+    want = oracle_all(po.OracleTrie.from_trie(t), beams, ids, lp, wl.RULES["c2"])
     print("C2 oracle:", result_stats(want), flush=True)
     yield t, beams, ids, lp, want
     t.clear()

@@ -24,7 +24,7 @@ def paper(ft, po):
     assert t.num_keys() == wl.PAPER_KEYS
     t.init_tbs_gpu(8, max_num_topk=1000, max_num_outpos=16, max_num_out_beams=1000,
                    max_num_out_tokens=16000, max_num_inter_beams=16000)
-    ot = wl.oracle(po, t)
+    ot = po.OracleTrie.from_trie(t)
     cases = {}
     for model, beam in CASES:
         beams, ids, lp = wl.requests(ft, t, "paper", model, 7000 * beam, N, beam)

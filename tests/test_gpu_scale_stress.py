@@ -22,7 +22,7 @@ def stress(ft, po):
     t.init_tbs_gpu(8, max_num_topk=1000, max_num_outpos=32, max_num_out_beams=1000,
                    max_num_out_tokens=32000, max_num_inter_beams=32000)
     beams, ids, lp = wl.requests(ft, t, "stress", "example", 0, N, 1000)
-    yield t, wl.oracle(po, t), beams, ids, lp
+    yield t, po.OracleTrie.from_trie(t), beams, ids, lp
     t.clear()
 
 

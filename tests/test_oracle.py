@@ -177,3 +177,18 @@ def test_variants_agree_on_regressions(po):
                                   c["early_exit"], variant=variant)
             assert sents == c["expect_sents"]
             assert [float(x).hex() for x in norms] == c["expect_norms_hex"]
+
+
+def test_from_trie_equals_from_keys(ft, po):
+    # the oracle over a flashtrie image (the scale tests' and the bench's
+    # way) searches exactly as the oracle built from the same keys
+    toks, offs = ft.synth_keys(3000, 512, 3, 7, 1.1, 5)
+    t = ft.Trie()
+    t.build_arrays(toks, offs)
+    a = po.OracleTrie.from_trie(t)
+    b = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 4, 512, 6, 24, 8, 0.3, 2.0, True, 5)
+    for r in range(4):
+        ra = a.tbs([8] * 6, ids[r], lp[r], -10.0, -40.0, 5.0, False)
+        rb = b.tbs([8] * 6, ids[r], lp[r], -10.0, -40.0, 5.0, False)
+        assert ra[0] == rb[0] and np.array_equal(ra[1], rb[1])
