@@ -101,6 +101,10 @@ struct ft_ctx {
   uint64_t louds_bytes = 0;
   uint32_t wdir_log2 = 0, wide_min = 0;
   uint64_t wide_nodes = 0, wide_buckets = 0, wide_failed = 0;
+  // root directory (null: none; FT_ROOT_DIR=0 turns it off, =force makes
+  // step 0 use it for a scanned root too)
+  RootEnt* d_root_dir = nullptr;
+  uint32_t root_n = 0, root_force = 0;
 
   std::vector<StagedReq> staged;
   // per request of a streamed search: taken, its error and error text
@@ -595,6 +599,47 @@ static int build_wide_index(ft_ctx* c, const uint8_t* image) {
   return FT_OK;
 }
 
+// The root directory (RootEnt): one entry per token below the root's
+// largest child token + 1, filled on the device by parent_entry of each
+// child at step 1.  None when the root has no child, a child token is
+// kRootDirMax or more, or FT_ROOT_DIR=0.
+static int build_root_dir(ft_ctx* c, const uint8_t* image) {
+  if (c->d_louds_words) return FT_OK;  // (the records' child ranges only)
+  if (const char* s = std::getenv("FT_ROOT_DIR")) {
+    if (std::strcmp(s, "0") == 0) return FT_OK;
+    if (std::strcmp(s, "force") == 0) c->root_force = 1;
+  }
+  const ft_node_rec* R = (const ft_node_rec*)(image + c->hdr.recs_offset);
+  const uint32_t c0 = R[0].child_begin, deg = R[1].child_begin - c0;
+  if (deg == 0) return FT_OK;
+  uint32_t top = 0;
+  for (uint32_t i = 0; i < deg; ++i) top = std::max(top, R[c0 + i].first_tok);
+  if (top >= kRootDirMax) return FT_OK;
+  const uint32_t n = top + 1;
+  hipError_t e;
+  if ((e = hipMalloc(&c->d_root_dir, (size_t)n * sizeof(RootEnt))) != hipSuccess)
+    return hip_fail(e, "hipMalloc(root directory)");
+  if ((e = hipMemsetAsync(c->d_root_dir, 0, (size_t)n * sizeof(RootEnt), c->stream)) !=
+      hipSuccess)
+    return hip_fail(e, "hipMemsetAsync(root directory)");
+  KArgs a{};
+  a.recs = (const ft_node_rec*)(c->d_image + c->hdr.recs_offset);
+  a.parent = (const uint32_t*)(c->d_image + c->hdr.parent_offset);
+  a.tail = (const uint32_t*)(c->d_image + c->hdr.tail_offset);
+  a.wdir = c->d_wdir;
+  a.wtab = c->d_wtab;
+  a.wfp = c->d_wfp;
+  a.labels = c->d_labels;
+  a.wdir_log2 = c->wdir_log2;
+  a.wide_min = c->wide_min;
+  if ((e = launch_root_dir(a, c->d_root_dir, n, c0, deg, c->stream)) != hipSuccess)
+    return hip_fail(e, "launch(root directory)");
+  if ((e = hipStreamSynchronize(c->stream)) != hipSuccess)
+    return hip_fail(e, "hipStreamSynchronize(root directory)");
+  c->root_n = n;
+  return FT_OK;
+}
+
 #ifndef FT_BUILD_ID
 #define FT_BUILD_ID "unknown"
 #endif
@@ -705,6 +750,10 @@ int ft_create(const void* image, size_t image_bytes, int device,
       return fail(FT_E_ARG, "ft_create: FT_CHILD_INDEX=louds is switched off (its kernel "
                             "faulted once and the cause is not found); use the node records");
     }
+  }
+  if (int rc = build_root_dir(c, (const uint8_t*)image)) {
+    ft_destroy(c);
+    return rc;
   }
   c->max_resident = tbs_max_resident_blocks(c->num_cus);
   if (c->max_resident <= 0) {
@@ -1308,6 +1357,9 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   a.out_host = nullptr;
   a.stage_bytes = 0;
   a.ready_ticks = c->ready_ticks;
+  a.root_dir = c->d_root_dir;
+  a.root_n = c->d_root_dir ? c->root_n : 0u;
+  a.root_force = c->root_force;
   return a;
 }
 
@@ -1855,6 +1907,7 @@ void ft_destroy(ft_ctx* c) {
   if (c->d_wtab) (void)hipFree(c->d_wtab);
   if (c->d_wfp) (void)hipFree(c->d_wfp);
   if (c->d_labels) (void)hipFree(c->d_labels);
+  if (c->d_root_dir) (void)hipFree(c->d_root_dir);
   if (c->d_louds_words) (void)hipFree(c->d_louds_words);
   if (c->d_louds_z) (void)hipFree(c->d_louds_z);
   if (c->d_louds_s) (void)hipFree(c->d_louds_s);

@@ -186,6 +186,34 @@ struct WideDirGroup {   // kDirSlots directory entries (device side)
 static_assert(sizeof(WideDirGroup) == 64, "WideDirGroup layout");
 constexpr uint32_t kWideFiltered = 1u;
 constexpr uint32_t kFpMaxLog2 = 16;
+
+// Root directory: the root's children indexed by their first token, one
+// 32-byte entry per token below the largest child token + 1.  Step 0 looks
+// a proposal up with one read of 8 bytes (node, flags) instead of a
+// fingerprint word and a 64-byte bucket, and its emit builds a survivor's
+// parent-table entry for step 1 from the same entry (one 32-byte read)
+// instead of the node's record, its table-directory group and, for a link
+// parent, its pending token.  Built on the device from parent_entry itself
+// at context creation; node 0 (the root, never a child) marks a token with
+// no child.
+struct RootEnt {
+  uint32_t node;      // the child, 0: none
+  uint32_t flags;     // kRd* | log2 table size << 8
+  uint32_t c0, deg;   // first child and degree of the child
+  uint32_t tab;       // its hash table's first bucket (kRdTable)
+  uint32_t link_tok;  // a link parent (kRdLink): its token of step 1
+  uint32_t link_lp;   // ... and that token's index in tail[] (or none)
+  uint32_t sd;        // its string depth
+};
+static_assert(sizeof(RootEnt) == 32, "RootEnt layout");
+constexpr uint32_t kRdSel = 1u;       // closes a key of length 1
+constexpr uint32_t kRdLink = 2u;      // a link parent at step 1
+constexpr uint32_t kRdTable = 4u;     // has a hash table
+constexpr uint32_t kRdFiltered = 8u;  // ... with fingerprint filtering
+constexpr uint32_t kRdErr = 16u;      // its entry could not be built
+// Largest directory built (entries); a root with larger child tokens keeps
+// its hash table or binary search.
+constexpr uint32_t kRootDirMax = 1u << 25;
 constexpr uint32_t kBucketSlots = 8;
 struct WideBucket {
   uint32_t tok[kBucketSlots];
@@ -293,6 +321,11 @@ struct KArgs {
   // how long a leader (or helper 1) waits for a ready word, in wall-clock
   // ticks: kReadyTicks, or less when a test asks for it
   uint64_t ready_ticks;
+  // the root directory (null: none) and its entries; root_force: step 0
+  // uses it even where the root's children would be scanned (tests)
+  const RootEnt* root_dir;
+  uint32_t root_n;
+  uint32_t root_force;
 };
 
 // LOUDS directory of the trie's shape: for every node v in breadth-first
@@ -311,6 +344,12 @@ constexpr uint32_t kLoudsBlockBits = 512;
 // `stream` (an ordinary launch: no workgroup waits for one that may not be
 // resident, see tbs_kernel.hip).
 hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
+
+// Fills the root directory `dir` (root_n entries, zeroed by the caller)
+// from the root's `deg` children starting at node c0, on `stream`.  `args`
+// needs the image and wide-index fields only.
+hipError_t launch_root_dir(const KArgs& args, RootEnt* dir, uint32_t root_n, uint32_t c0,
+                           uint32_t deg, hipStream_t stream);
 
 // The no-allocation scratch: one file-scope device array of this many
 // bytes per device, holding a search's staged requests, outputs and

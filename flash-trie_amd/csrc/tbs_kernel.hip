@@ -219,7 +219,8 @@ enum : uint8_t {
   M_LP_SEL = 2,
   M_SCAN = 3,
   M_SEARCH = 4,
-  M_HASH = 5
+  M_HASH = 5,
+  M_DENSE = 6  // the root at step 0: its children from the root directory
 };
 
 __device__ __forceinline__ uint64_t norm_key(double v) {
@@ -279,6 +280,19 @@ __device__ __forceinline__ uint64_t row_reduce64(uint64_t v, bool take_min) {
   v = take_min ? min(v, y) : max(v, y);
   y = dpp_move64<0x121>(v);           // row_ror:1
   return take_min ? min(v, y) : max(v, y);
+}
+// Sum of x over the 64 lanes of a wave, in every lane; every lane must be
+// active.  Rotations by 8, 4, 2, 1 within each row of 16 lanes, then the
+// four row sums.
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+  x += dpp_move<0x128>(x);  // row_ror:8
+  x += dpp_move<0x124>(x);  // row_ror:4
+  x += dpp_move<0x122>(x);  // row_ror:2
+  x += dpp_move<0x121>(x);  // row_ror:1
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 0) +
+         (uint32_t)__builtin_amdgcn_readlane((int)x, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)x, 32) +
+         (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
 }
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
   const uint32_t lane = lane_id(), rl = lane & 15u;
@@ -865,6 +879,39 @@ __device__ __forceinline__ ParEntry parent_entry(const KArgs& a, uint32_t node, 
   return e;
 }
 
+// parent_entry(node, 1, K) of a root child from its root-directory entry
+// (x: node, flags, c0, deg; y: tab, link_tok, link_lp, sd): the same
+// branches, with the scan limit of this launch.
+__device__ __forceinline__ ParEntry root_child_entry(const KArgs& a, const uint4 x,
+                                                     const uint4 y, uint32_t K) {
+  const uint32_t f = x.y, deg = x.w, sd = y.w;
+  ParEntry e{x.z, deg, (uint32_t)M_NONE, 0u, kNoCursor};
+  if (f & kRdLink) {
+    e.c0 = sd;
+    e.aux = y.y;
+    e.mode = (sd == 2u) ? M_LP_SEL : M_LP_NEXT;
+    e.work = 1;
+    e.lp = y.z;
+  } else if (deg == 0) {
+    e.mode = M_NONE;
+  } else if (deg <= a.scan_limit) {
+    e.mode = M_SCAN;
+    e.work = deg;
+  } else {
+    e.mode = M_SEARCH;
+    e.work = K;
+    if (f & kRdTable) {
+      e.mode = M_HASH | ((f & kRdFiltered) ? kModeFiltered : 0u);
+      e.aux = (f >> 8) & 0xFFu;
+      e.c0 = y.x;
+    }
+  }
+  if ((e.mode & kModeMask) == M_SCAN || (e.mode & kModeMask) == M_HASH) {
+    if (sd == 1u) e.mode |= kModeDepthOk;
+  }
+  return e;
+}
+
 // Work items of a parent-table entry.
 __device__ __forceinline__ uint32_t entry_work(uint32_t mode, uint32_t aux, uint32_t K) {
   switch (mode & kModeMask) {
@@ -872,7 +919,8 @@ __device__ __forceinline__ uint32_t entry_work(uint32_t mode, uint32_t aux, uint
     case M_LP_SEL: return 1u;
     case M_SCAN: return aux;
     case M_SEARCH:
-    case M_HASH: return K;
+    case M_HASH:
+    case M_DENSE: return K;
     default: return 0u;
   }
 }
@@ -1126,7 +1174,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
         ftok = lw & kTokMask;
         have_child = true;
         label_sel = (lw & kSlotSel) && depth_ok;
-      } else if (md == M_SEARCH || md == M_HASH) {
+      } else if (md == M_SEARCH || md == M_HASH || md == M_DENSE) {
         pos = (int)q;
       }
       if (ftok != kNoToken)
@@ -1207,6 +1255,17 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
               have_child = true;
               label_sel = (hw & kSlotSel) && depth_ok;
             }
+          } else if (md == M_DENSE) {
+            // the root's child of this token: one read of (node, flags)
+            if (tok < a.root_n) {
+              const uint2 rd = *(const uint2*)&a.root_dir[tok];
+              ++my_probes;
+              if (rd.x != 0u) {
+                cnode = rd.x;
+                have_child = true;
+                label_sel = (rd.y & kRdSel) && depth_ok;
+              }
+            }
           }
           if (md == M_LP_NEXT) {
             do_next = true;
@@ -1257,8 +1316,15 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
       }
     }
   }
-  if (my_children) atomicAdd(&sm.w_children, my_children);
-  if (my_probes) atomicAdd(&sm.w_probes, my_probes);
+  // the workgroup's counters: one LDS add a wave (lane by lane, the adds to
+  // one word would run one after another, 1024 of them)
+  {
+    const uint32_t wc = wave_sum(my_children), wp = wave_sum(my_probes);
+    if ((tid & 63u) == 0u) {
+      if (wc) atomicAdd(&sm.w_children, wc);
+      if (wp) atomicAdd(&sm.w_probes, wp);
+    }
+  }
   __syncthreads();
   // the buffered pushes: one global append per list (a solo workgroup's
   // lists start at 0)
@@ -2172,7 +2238,18 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
   }
   uint32_t root_err = 0;
   if (tid == 64u) {
-    const ParEntry e = parent_entry<kLouds>(a, 0u, 0u, K, &root_err);
+    ParEntry e = parent_entry<kLouds>(a, 0u, 0u, K, &root_err);
+    if (a.root_dir) {
+      // a root searched or hashed (or scanned, when forced) looks its
+      // children up in the root directory instead; a one-token child
+      // closes a key of length 1 when the root's string depth is 0
+      const uint32_t m = e.mode & kModeMask;
+      if (m == M_SEARCH || m == M_HASH || (m == M_SCAN && a.root_force)) {
+        const bool dok = (a.recs[0].meta & FT_META_DEPTH_MASK) == 0u;
+        e.mode = M_DENSE | (dok ? kModeDepthOk : 0u);
+        e.work = K;
+      }
+    }
     st_dev(&par_c0[0], e.c0);
     st_dev(&par_aux[0], e.aux);
     st_dev(&par_node[0], 0u);
@@ -2733,6 +2810,12 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
           e.mode = (t + 2 == xsd) ? M_LP_SEL : M_LP_NEXT;
           e.work = 1;
           e.lp = sm.x_tc[j] + 1u;
+        } else if (t == 0u && tk < a.root_n) {
+          // a child of the root: its entry from the root directory
+          const uint4* rp = (const uint4*)&a.root_dir[tk];
+          const uint4 rx = rp[0], ry = rp[1];
+          if (rx.x == c.node && !(rx.y & kRdErr)) e = root_child_entry(a, rx, ry, K);
+          else e = parent_entry<kLouds>(a, c.node, t + 1, K, &err);
         } else {
           e = parent_entry<kLouds>(a, c.node, t + 1, K, &err);
         }
@@ -3037,6 +3120,49 @@ hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
   } else {
     hipLaunchKernelGGL((tbs_kernel<false, false>), grid, block, 0, stream, args);
   }
+  return hipGetLastError();
+}
+
+// One thread per root child: its root-directory entry, from parent_entry at
+// step 1 with scan limit 0 (so that a child with a hash table reports it;
+// the search picks scan or lookup with its own limit, root_child_entry).
+__global__ void __launch_bounds__(256) root_dir_kernel(KArgs a, RootEnt* dir, uint32_t root_n,
+                                                       uint32_t c0, uint32_t deg) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= deg) return;
+  const uint32_t ch = c0 + i;
+  const ft_node_rec r = a.recs[ch];
+  if (r.first_tok >= root_n) return;  // (the host sized the directory on these tokens)
+  uint32_t err = 0;
+  const ParEntry e = parent_entry<false>(a, ch, 1u, 1u, &err);
+  const uint32_t sd = r.meta & FT_META_DEPTH_MASK;
+  const uint32_t el = (r.meta >> FT_META_ELEN_SHIFT) & FT_META_ELEN_MASK;
+  const bool link = (r.meta & FT_META_TERMINAL) && sd > 1u;
+  uint32_t f = 0;
+  if ((r.meta & FT_META_TERMINAL) && el == 1u) f |= kRdSel;
+  if (link) f |= kRdLink;
+  if ((e.mode & kModeMask) == M_HASH)
+    f |= kRdTable | ((e.mode & kModeFiltered) ? kRdFiltered : 0u) | ((e.aux & 0xFFu) << 8);
+  if (err) f |= kRdErr;
+  RootEnt o;
+  o.node = ch;
+  o.flags = f;
+  o.c0 = r.child_begin;
+  o.deg = a.recs[ch + 1].child_begin - r.child_begin;
+  o.tab = (f & kRdTable) ? e.c0 : 0u;
+  o.link_tok = link ? e.aux : 0u;
+  o.link_lp = link ? e.lp : kNoCursor;
+  o.sd = sd;
+  dir[r.first_tok] = o;
+}
+
+hipError_t launch_root_dir(const KArgs& args, RootEnt* dir, uint32_t root_n, uint32_t c0,
+                           uint32_t deg, hipStream_t stream) {
+  if (deg == 0) return hipSuccess;
+  KArgs a = args;
+  a.scan_limit = 0;
+  hipLaunchKernelGGL(root_dir_kernel, dim3((deg + 255u) / 256u), dim3(256), 0, stream, a, dir,
+                     root_n, c0, deg);
   return hipGetLastError();
 }
 

@@ -306,6 +306,56 @@ def test_request_errors(ft, c1):
     assert_same_results((got[0][0], got[1][0]), want)
 
 
+def test_conversion_errors_come_first(ft, c1):
+    """An element that cannot be converted raises the conversion's error
+    (TypeError, as pybind11's caster does), before any search error of the
+    batch: a plan error of a later request, or a packing error of an
+    earlier one; a ragged row raises marisa::Trie's shape error; the next
+    call is unaffected."""
+    t, o, ids, lp = c1
+    rows = [ids[r].tolist() for r in range(8)]
+    lps = [lp[r].tolist() for r in range(8)]
+    beams = [[10] * 8 for _ in range(8)]
+
+    def with_text(r):
+        bad = [list(x) for x in rows[r]]
+        bad[3][4] = "7"
+        return bad
+
+    print("conversion error alone", flush=True)
+    bi = list(rows)
+    bi[3] = with_text(3)
+    with pytest.raises(TypeError, match="incompatible arguments"):
+        ft.bs_tbs_gpu(t, 8, beams, bi, lps, -10.0, -40.0, 5.0, False)
+    print("conversion error before a later request's plan error", flush=True)
+    bi = list(rows)
+    bi[2] = with_text(2)
+    bb = [list(b) for b in beams]
+    bb[5] = [11] * 8  # above max_num_out_beams
+    with pytest.raises(TypeError, match="incompatible arguments"):
+        ft.bs_tbs_gpu(t, 8, bb, bi, lps, -10.0, -40.0, 5.0, False)
+    print("conversion error after an earlier request's packing error", flush=True)
+    bi = list(rows)
+    bi[6] = with_text(6)
+    bl = list(lps)
+    nan = lp[1].copy()
+    nan[2, 7] = np.nan
+    bl[1] = nan.tolist()
+    with pytest.raises(TypeError, match="incompatible arguments"):
+        ft.bs_tbs_gpu(t, 8, beams, bi, bl, -10.0, -40.0, 5.0, False)
+    print("ragged row in a converted request", flush=True)
+    bi = list(rows)
+    bi[4] = [list(x) for x in rows[4]]
+    bi[4][5] = bi[4][5][:-1]
+    with pytest.raises(RuntimeError, match="ragged"):
+        ft.bs_tbs_gpu(t, 8, beams, bi, lps, -10.0, -40.0, 5.0, False)
+    print("after the errors", flush=True)
+    s, n, _, _ = ft.bs_tbs_gpu(t, 8, beams, rows, lps, -10.0, -40.0, 5.0, False)
+    for i in range(8):
+        want = o.tbs([10] * 8, ids[i], lp[i], -10.0, -40.0, 5.0, False)
+        assert_same_results((s[i], n[i]), want, f"after the errors, {i}")
+
+
 @pytest.mark.parametrize("early", [False, True])
 def test_streamed_batches(ft, c1, early):
     # bs_tbs_gpu packs each request after the launch and the kernel picks it
@@ -667,6 +717,70 @@ def test_louds_child_index_is_switched_off(ft, monkeypatch):
     with pytest.raises(RuntimeError, match="switched off"):
         t.init_tbs_gpu(1, max_num_topk=4, max_num_outpos=2, max_num_out_beams=2,
                        max_num_out_tokens=4, max_num_inter_beams=8)
+
+
+@pytest.mark.parametrize("root_dir,scan_mult,wide_min", [
+    ("force", "2", "64"), ("force", "0", "2"), ("force", "999999", "512"),
+    ("0", "2", "64"), ("0", "0", "2")])
+def test_root_directory(ft, po, monkeypatch, root_dir, scan_mult, wide_min):
+    # Step 0 looks the root's children up in the token-indexed root
+    # directory (forced here for a scanned root too) and builds step 1's
+    # parent table from it -- for children that are scanned, searched,
+    # hashed and link parents alike -- or, with FT_ROOT_DIR=0, from the
+    # node records and tables as every later step does.  Both equal the
+    # oracle, on tiny tries with ties and on a wider one.
+    monkeypatch.setenv("FT_ROOT_DIR", root_dir)
+    monkeypatch.setenv("FT_SCAN_MULT", scan_mult)
+    monkeypatch.setenv("FT_WIDE_MIN", wide_min)
+    rng = np.random.default_rng(11)
+    for case in range(30):
+        vocab = int(rng.integers(2, 10))
+        keys = sorted({tuple(rng.integers(0, vocab, int(rng.integers(1, 7))))
+                       for _ in range(int(rng.integers(1, 40)))})
+        keys = [list(map(int, k)) for k in keys]
+        T = int(rng.integers(1, 8))
+        K = int(rng.integers(1, vocab + 1))
+        ids = np.stack([np.sort(rng.choice(vocab, K, replace=False))
+                        for _ in range(T)]).astype(np.uint32)
+        lp = (-rng.integers(0, 8, (T, K)) * 0.5).astype(np.float32)
+        beams = [int(rng.integers(1, 6)) for _ in range(T)]
+        early = bool(rng.integers(0, 2))
+        print("root directory", root_dir, scan_mult, wide_min, "tiny case", case, flush=True)
+        t = _gpu_trie(ft, keys=keys, batch=1, topk=16, steps=8, beams=8)
+        got = ft.bs_tbs_gpu(t, 1, [beams], [ids.tolist()], [lp.tolist()],
+                            -3.0, -9.0, 1.0, early)
+        want = po.OracleTrie.from_keys(keys).tbs(beams, ids, lp, -3.0, -9.0, 1.0, early)
+        assert_same_results((got[0][0], got[1][0]), want, f"tiny case {case}")
+    toks, offs = ft.synth_keys(50000, 4096, 3, 8, 1.1, 5)
+    t = _gpu_trie(ft, toks=toks, offs=offs, batch=4, topk=32, steps=8,
+                  beams=16, inter=2048)
+    o = po.OracleTrie.from_keys(toks=toks, offs=offs)
+    ids, lp = ft.synth_requests(t, 0, 16, 4096, 8, 32, 16, 0.3, 2.0, True, 5, model=1)
+    for b0 in range(0, 16, 4):
+        print("root directory", root_dir, scan_mult, wide_min, "requests", b0, flush=True)
+        got = ft.bs_tbs_gpu(t, 4, [[16] * 8] * 4,
+                            [ids[b0 + i].tolist() for i in range(4)],
+                            [lp[b0 + i].tolist() for i in range(4)],
+                            -10.0, -40.0, 5.0, b0 == 8)
+        for i in range(4):
+            want = o.tbs([16] * 8, ids[b0 + i], lp[b0 + i], -10.0, -40.0, 5.0, b0 == 8)
+            assert_same_results((got[0][i], got[1][i]), want, f"request {b0 + i}")
+
+
+def test_root_tokens_beyond_the_directory(ft, po):
+    # a root child token of 2^25 or more: no root directory, the root's
+    # table or search as before
+    keys = [[1, 2], [1, 3], [5], [(1 << 25) + 7, 2], [(1 << 30), 4, 4]]
+    t = _gpu_trie(ft, keys=keys, batch=1, topk=4, steps=3, beams=4)
+    ids = np.array([[1, 5, (1 << 25) + 7, 1 << 30], [2, 3, 4, 9], [4, 5, 6, 7]], np.uint32)
+    lp = np.array([[-0.5, -1.0, -0.25, -2.0], [-0.1, -0.2, -0.3, -0.4],
+                   [-1.0, -1.5, -2.0, -2.5]], np.float32)
+    for early in (False, True):
+        print("large root tokens, early", early, flush=True)
+        got = ft.bs_tbs_gpu(t, 1, [[4, 4, 4]], [ids.tolist()], [lp.tolist()],
+                            -10.0, -40.0, 1.0, early)
+        want = po.OracleTrie.from_keys(keys).tbs([4, 4, 4], ids, lp, -10.0, -40.0, 1.0, early)
+        assert_same_results((got[0][0], got[1][0]), want, f"early {early}")
 
 
 def test_topk_limit(ft):
