@@ -22,6 +22,9 @@ store seen on another XCD, L_post):
                 gather pass over the pushes)
                 emit: L_l2 (the push) + 2 L_img (the node record, then the
                 pending token of a link parent)
+  step 0        with the root directory (a root that is not scanned, and
+                FT_ROOT_DIR not 0): expansion L_img (the token's entry),
+                emit 2 L_l2 (the push, then the same entry again)
   tail step     L_l2 / 4 (a round of up to four steps reads its rows once)
   start         L_img (the root's entry) ; output: (mean length / 2 + 1)
                 L_l2 (the history walk, two tokens a record)
@@ -122,10 +125,11 @@ def main():
         general = ss[:, t, 5].max() > 0
         shared = m[8] > 0 or m[9] > 0
         cut = m[2] > ss[:, min(t + 1, T - 1), 0].mean() + 0.5 if t + 1 < T else False
+        root_dir = t == 0 and m[6] == 0 and os.environ.get("FT_ROOT_DIR", "") != "0"
         if general:
-            fe = L_img * (2 if m[7] > 0 else 1) + (2 * L_post if shared else 0.0)
+            fe = L_img * (2 if m[7] > 0 and not root_dir else 1) + (2 * L_post if shared else 0.0)
             fs = 2 * L_l2 if cut else 0.0
-            fm = L_l2 + 2 * L_img
+            fm = 2 * L_l2 if root_dir else L_l2 + 2 * L_img
         else:
             fe, fs, fm = L_l2 / 4, 0.0, 0.0
         floor += fe + fs + fm
