@@ -818,6 +818,7 @@ static uint64_t ws_layout(uint64_t B, uint64_t K, uint64_t hist, uint32_t slots,
   L.par_mode = off; off = align_up(off + B * 4, 256);
   L.par_woff = off; off = align_up(off + (B + 1) * 4, 256);
   L.claims = off; off = align_up(off + (uint64_t)slots * 8, 256);
+  L.dones = off; off = align_up(off + (uint64_t)slots * 16, 256);
   L.claim_slots = slots;
   L.next_cap = (uint32_t)BK;
   L.sel_cap = (uint32_t)(BK + B);
@@ -1880,9 +1881,9 @@ int ft_search_noalloc(ft_ctx* c, const ft_request* reqs, size_t batch,
   uint8_t* base = c->d_scratch;
   hipError_t e = hipMemcpyAsync(base, g_na_stage, used, hipMemcpyHostToDevice, c->stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(scratch stage)");
-  // the control blocks and claim words start at "nothing posted" (a fill
-  // kernel, no memset)
-  if ((e = clear_controls(base + ws_off, ws_stride, L.ctl, L.claims, L.claim_slots,
+  // the control blocks, claim words and done words start at "nothing
+  // posted" (a fill kernel, no memset)
+  if ((e = clear_controls(base + ws_off, ws_stride, L.ctl, L.claims, L.dones, L.claim_slots,
                           (uint32_t)batch, c->stream)) != hipSuccess)
     return hip_fail(e, "clear_controls");
   const KArgs a = kernel_args(c, base, 0, batch, (uint32_t)K, base + ws_off, ws_stride, L,

@@ -244,19 +244,19 @@ __host__ __device__ inline uint32_t cuckoo_h2(uint32_t tok, uint32_t lg) {
 }
 
 // Per-request control block shared by the request's leader and helper
-// workgroups.  `go` and `done` sit on their own 128-byte lines.
+// workgroups.  `go` sits on its own 128-byte line.
 constexpr uint32_t kGoExit = 0xFFFFFFFFu;
 struct Ctl {
   unsigned long long go;  // (launch epoch << 32) | generation of the shared step
   uint32_t pad0[30];
-  uint32_t done;          // helpers finished with the current shared step
-  uint32_t pad1[31];
+  uint32_t pad1[32];
   // the shared step, written by the leader before `go`
   uint32_t t, W, n_par, nS;
   uint32_t sel_which, cur_which, status, pad2;
-  // counters of the step (atomics)
-  uint32_t n_next, n_sel;
-  unsigned long long children, probes;
+  // pushes of the step into `next` (low 32 bits) and `selected` (high 32
+  // bits): one 64-bit atomic add a workgroup
+  unsigned long long pushes;
+  unsigned long long pad4[2];
   // streamed search: the copy of the rows after the first ready word's
   // (launch epoch << 32) | kCopy* state, claimed by helper 1 or the leader
   unsigned long long copy;
@@ -270,6 +270,10 @@ struct WsLayout {   // byte offsets inside one request's workspace slot
   // claim words of a shared step's slices, one per workgroup of the
   // request: (launch epoch << 32) | generation of the step it was taken for
   uint64_t claims;
+  // done words, 16 bytes per workgroup: the (epoch, generation) of the last
+  // shared step whose slice it finished, then its children scanned (low
+  // 32 bits) and buckets read (high) in that slice, written before it
+  uint64_t dones;
   uint32_t next_cap, sel_cap, hist_cap, cur_cap;
   uint32_t claim_slots, pad;
 };
@@ -361,10 +365,12 @@ constexpr uint64_t kScratchBytes = 128ull << 20;
 // kept; later calls return the kept address.
 hipError_t scratch_address(int device, void** ptr);
 
-// Zeroes the control block (Ctl, at byte ctl_off) and the claim words
-// (claim_slots of them at claims_off) of `count` workspace slots of
-// `stride` bytes from `ws`, with a fill kernel on `stream`.
+// Zeroes the control block (Ctl, at byte ctl_off), the claim words
+// (claim_slots of them at claims_off) and the done words (2 * claim_slots
+// at dones_off) of `count` workspace slots of `stride` bytes from `ws`,
+// with a fill kernel on `stream`.
 hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64_t claims_off,
+                          uint64_t dones_off,
                           uint32_t claim_slots, uint32_t count, hipStream_t stream);
 
 // Workgroups of the search kernel that fit on the device at once.

@@ -253,6 +253,24 @@ __device__ __forceinline__ uint32_t wave_append(bool want, uint32_t* ctr) {
   return base + lanemask_lt_count(m);
 }
 
+// wave_append on one half of a 64-bit counter pair (high: the upper 32
+// bits), one 64-bit add for the wave; the halves never carry into each
+// other (each stays below 2^32).
+__device__ __forceinline__ uint32_t wave_append_half(bool want, unsigned long long* ctr,
+                                                     bool high) {
+  const uint64_t m = __ballot(want);
+  if (m == 0) return 0;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  uint32_t base = 0;
+  if ((int)lane_id() == leader) {
+    const unsigned long long old =
+        atomicAdd(ctr, (unsigned long long)__popcll(m) << (high ? 32 : 0));
+    base = high ? (uint32_t)(old >> 32) : (uint32_t)old;
+  }
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
+  return base + lanemask_lt_count(m);
+}
+
 // Inclusive scan of x over the 64 lanes of a wave; every lane must be
 // active.  Lane moves are DPP operands of the adds (no LDS round trip):
 // shifts by 1, 2, 4, 8 within each row of 16 lanes, then lane 15 of each
@@ -1286,7 +1304,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
     if (__ballot(do_next)) {
       const uint32_t li = wave_append(do_next, &sm.lq_next);
       const bool spill = do_next && li >= (uint32_t)kPushCap;
-      const uint32_t gi = solo ? li : wave_append(spill, &v.ctl->n_next);
+      const uint32_t gi = solo ? li : wave_append_half(spill, &v.ctl->pushes, false);
       if (do_next) {
         const uint64_t key = norm_key(s2 * v.lnf_next);
         if (!spill) {
@@ -1301,7 +1319,7 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
     if (__ballot(do_sel)) {
       const uint32_t li = wave_append(do_sel, &sm.lq_sel);
       const bool spill = do_sel && li >= (uint32_t)kPushSelCap;
-      const uint32_t gi = solo ? li : wave_append(spill, &v.ctl->n_sel);
+      const uint32_t gi = solo ? li : wave_append_half(spill, &v.ctl->pushes, true);
       if (do_sel) {
         SelRec sr;
         sr.s = s2;
@@ -1332,11 +1350,14 @@ __device__ __forceinline__ void expand_range(const KArgs& a, const StepView& v, 
   const uint32_t sl = min(sm.lq_sel, (uint32_t)kPushSelCap);
   uint32_t gb_next = 0, gb_sel = 0;
   if (!solo) {
+    // both lists' places in one 64-bit add (every workgroup of the step
+    // adds to this word: one add each, not one per list and counter)
     if (tid == 0) {
-      if (sm.w_children) atomicAdd(&v.ctl->children, (unsigned long long)sm.w_children);
-      if (sm.w_probes) atomicAdd(&v.ctl->probes, (unsigned long long)sm.w_probes);
-      sm.gb_next = nl ? atomicAdd(&v.ctl->n_next, nl) : 0u;
-      sm.gb_sel = sl ? atomicAdd(&v.ctl->n_sel, sl) : 0u;
+      unsigned long long old = 0;
+      if (nl || sl)
+        old = atomicAdd(&v.ctl->pushes, (unsigned long long)nl | ((unsigned long long)sl << 32));
+      sm.gb_next = (uint32_t)old;
+      sm.gb_sel = (uint32_t)(old >> 32);
     }
     __syncthreads();
     gb_next = sm.gb_next;
@@ -1724,8 +1745,14 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     if ((v >> 32) != a.epoch || (uint32_t)v == kGoExit || v == seen) return;
     seen = v;
     if (mine == 0) continue;  // the leader took this slice over
+    // this workgroup's done word (its counters, then the step's tag)
+    unsigned long long* dw = (unsigned long long*)(ws + a.lay.dones) + 2ull * g;
     if (mine == 2) {          // (never for a posted step)
-      if (tid == 0) atomicAdd(&ctl->done, 1u);
+      if (tid == 0) {
+        st_dev(dw + 1, 0ull);
+        wait_stores();
+        st_dev(dw, v);
+      }
       continue;
     }
     StepView sv;
@@ -1809,9 +1836,10 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
                  hashed, sm);
     // the row lookups are done: empty the hash for the next step
     if (hashed) row_hash_clear(sm);
+    if (tid == 0) st_dev(dw + 1, pack2(sm.w_children, sm.w_probes));
     wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
-    if (tid == 0) atomicAdd(&ctl->done, 1u);
+    if (tid == 0) st_dev(dw, v);  // then its done word: no shared counter
   }
 }
 
@@ -2464,17 +2492,13 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
       // publish the step (the helpers read the row from the staged request),
       // then wake the helpers
       if (tid == 0) {
-        st_dev(&ctl->n_next, 0u);
-        st_dev(&ctl->n_sel, 0u);
-        st_dev(&ctl->children, 0ull);
-        st_dev(&ctl->probes, 0ull);
+        st_dev(&ctl->pushes, 0ull);
         st_dev(&ctl->t, t);
         st_dev(&ctl->W, W);
         st_dev(&ctl->n_par, n_cur);
         st_dev(&ctl->nS, nS);
         st_dev(&ctl->sel_which, sel_which);
         st_dev(&ctl->cur_which, cur_which);
-        st_dev(&ctl->done, 0u);
       }
       wait_stores();  // the step's data is complete before `go` moves
       __syncthreads();
@@ -2498,6 +2522,8 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
     }
     expand_range(a, sv, W, 0, (shared ? a.wgs : 1u) * (uint32_t)kWaves, true, !shared,
                  hashed, sm);
+    // (shared) the pushes of the step; the counters of the leader's slices
+    uint32_t sh_next = 0, sh_sel = 0, lead_ch = sm.w_children, lead_pr = sm.w_probes;
     if (shared) {
       // The helpers' slices: each is claimed by its helper (its claim word
       // set to this step) or, once kGraceTicks have passed since the post,
@@ -2524,6 +2550,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         __builtin_amdgcn_s_sleep(2);
       }
       uint32_t n_stolen = 0;
+      bool stole = false;  // (thread i) slice i + 1 was taken over here
       // (thread 0 alone knows whether helper 1 is copying: the takeover
       // runs when any slot is still pending or helper 1 copies)
       if (__syncthreads_or(pending_any || copying1)) {
@@ -2534,6 +2561,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         // a helper raised first stays the helper's
         if (tid < nh && (pending_any || tid == 0) &&
             atomicMax(&claims[tid + 1], mygo) < mygo) {
+          stole = true;
           const uint32_t k = atomicAdd(&sm.n_stolen, 1u);
           sm.stolen[k] = (uint16_t)(tid + 1);
         }
@@ -2552,30 +2580,55 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         __syncthreads();
         expand_range(a, sv, W, slice * (uint32_t)kWaves, a.wgs * (uint32_t)kWaves, true, false,
                      hashed, sm);
+        lead_ch += sm.w_children;
+        lead_pr += sm.w_probes;
+      }
+      // Every slice a helper claimed: thread i waits for helper i + 1's done
+      // word to carry this step's tag (written after its pushes and its
+      // counters are complete), unless thread i took that slice over.
+      const unsigned long long tw1 = wall_clock64();
+      unsigned long long* dones = (unsigned long long*)(ws + a.lay.dones);
+      const bool waits = tid < nh && !stole;
+      bool all_done = false;
+      for (uint32_t it = 0; it < kSpinLimit; ++it) {
+        if (__syncthreads_count(waits && ld_relaxed(&dones[2 * (tid + 1)]) != mygo) == 0) {
+          all_done = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
       }
       if (tid == 0) {
-        const unsigned long long tw1 = wall_clock64();
-        const uint32_t helped = nh - n_stolen;
-        for (uint32_t it = 0; it < kSpinLimit; ++it) {
-          if (ld_relaxed(&ctl->done) >= helped) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-        if (ld_relaxed(&ctl->done) < helped) sm.status |= kStatusCorrupt;
+        if (!all_done) sm.status |= kStatusCorrupt;
         if (t < d.out_T) {
           uint64_t* row = step_stats + (uint64_t)t * kStepStats;
           row[8] = tw1 - tw0;
           row[9] = wall_clock64() - tw1;
         }
       }
+      // the helpers' counters and the step's push counts, read together
+      const unsigned long long cw = waits ? ld_relaxed(&dones[2 * (tid + 1) + 1]) : 0ull;
+      const unsigned long long pw = ld_relaxed(&ctl->pushes);
+      sh_next = (uint32_t)pw;
+      sh_sel = (uint32_t)(pw >> 32);
+      const uint32_t wc = wave_sum((uint32_t)cw), wp = wave_sum((uint32_t)(cw >> 32));
+      if (tid == 0) {
+        sm.w_children = lead_ch;
+        sm.w_probes = lead_pr;
+      }
+      __syncthreads();
+      if ((tid & 63u) == 0u) {
+        if (wc) atomicAdd(&sm.w_children, wc);
+        if (wp) atomicAdd(&sm.w_probes, wp);
+      }
     }
     __syncthreads();
     // the helpers' pushes are complete (they waited for their stores before
-    // counting themselves done): drop stale cached copies before reading
+    // writing their done words): drop stale cached copies before reading
     if (shared) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const uint32_t n_next = shared ? ld_relaxed(&ctl->n_next) : sm.lq_next;
-    const uint32_t n_new = shared ? ld_relaxed(&ctl->n_sel) : sm.lq_sel;
-    const unsigned long long w_ch = shared ? ld_relaxed(&ctl->children) : sm.w_children;
-    const unsigned long long w_pr = shared ? ld_relaxed(&ctl->probes) : sm.w_probes;
+    const uint32_t n_next = shared ? sh_next : sm.lq_next;
+    const uint32_t n_new = shared ? sh_sel : sm.lq_sel;
+    const unsigned long long w_ch = sm.w_children;
+    const unsigned long long w_pr = sm.w_probes;
     // every writer of the status has passed the barrier above; only thread
     // 0 adds the overflow bit below, which every thread derives itself
     const bool overflow = n_next > next_cap || nS + n_new > sel_cap;
@@ -3086,23 +3139,26 @@ hipError_t scratch_address(int device, void** ptr) {
   return hipSuccess;
 }
 
-// One workgroup per slot: the slot's control block and claim words, word
-// by word.
+// One workgroup per slot: the slot's control block, claim words and done
+// words, word by word.
 __global__ void __launch_bounds__(128) clear_ctl_kernel(uint8_t* ws, uint64_t stride,
                                                         uint64_t ctl_off, uint64_t claims_off,
-                                                        uint32_t claim_slots) {
+                                                        uint64_t dones_off, uint32_t claim_slots) {
   uint8_t* slot = ws + (uint64_t)blockIdx.x * stride;
   uint32_t* p = (uint32_t*)(slot + ctl_off);
   for (uint32_t i = threadIdx.x; i < (uint32_t)(sizeof(Ctl) / 4); i += blockDim.x) p[i] = 0u;
   unsigned long long* c = (unsigned long long*)(slot + claims_off);
   for (uint32_t i = threadIdx.x; i < claim_slots; i += blockDim.x) c[i] = 0ull;
+  unsigned long long* dn = (unsigned long long*)(slot + dones_off);
+  for (uint32_t i = threadIdx.x; i < 2u * claim_slots; i += blockDim.x) dn[i] = 0ull;
 }
 
 hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64_t claims_off,
-                          uint32_t claim_slots, uint32_t count, hipStream_t stream) {
+                          uint64_t dones_off, uint32_t claim_slots, uint32_t count,
+                          hipStream_t stream) {
   if (count == 0) return hipSuccess;
   hipLaunchKernelGGL(clear_ctl_kernel, dim3(count), dim3(128), 0, stream, ws, stride, ctl_off,
-                     claims_off, claim_slots);
+                     claims_off, dones_off, claim_slots);
   return hipGetLastError();
 }
 

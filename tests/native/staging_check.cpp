@@ -16,7 +16,7 @@ hipError_t launch_tbs(const KArgs&, hipStream_t) { return hipErrorUnknown; }
 hipError_t launch_root_dir(const KArgs&, RootEnt*, uint32_t, uint32_t, uint32_t, hipStream_t) {
   return hipErrorUnknown;
 }
-hipError_t clear_controls(uint8_t*, uint64_t, uint64_t, uint64_t, uint32_t, uint32_t,
+hipError_t clear_controls(uint8_t*, uint64_t, uint64_t, uint64_t, uint64_t, uint32_t, uint32_t,
                           hipStream_t) {
   return hipErrorUnknown;
 }
