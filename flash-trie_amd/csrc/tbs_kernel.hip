@@ -41,6 +41,7 @@
 
 #include <mutex>
 
+#include "coherent.h"
 #include "tbs_kernel.h"
 
 namespace ftk {
@@ -981,32 +982,8 @@ __device__ __forceinline__ int row_find(const Smem& sm, uint32_t K,
 // which re-reads the pushes many times during selection, instead invalidates
 // its caches once per step (an acquire fence) and then reads normally.
 //
-// What this rests on is the code LLVM generates for gfx942-class targets
-// (gfx950 included) from monotonic agent-scope atomics -- the "Memory Model
-// GFX942" table of LLVM's AMDGPUUsage: a load is `global_load ... sc1`, a
-// store `global_store ... sc1`, each served at the coherence point of the
-// agent rather than from a possibly stale non-coherent line; and on the
-// ordering the hardware gives a wave: memory operations issue in program
-// order, `s_waitcnt vmcnt(0)` returns only once every earlier store has
-// been acknowledged, and no load after a branch on a loaded value issues
-// before that value is back.  Under the C++ memory model alone relaxed
-// atomics would not order the data against the flag; release / acquire
-// would, but their agent-scope form writes back / invalidates the L2 of the
-// XCD (buffer_wbl2 sc1 / buffer_inv sc1), which measured ~50% of step-1
-// time when every helper did it every step.  The inline `s_waitcnt` below
-// carries a memory clobber, so the compiler keeps the stores before it.
-__device__ __forceinline__ unsigned long long ld_relaxed(const unsigned long long* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_relaxed(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// The loads, stores and store wait this goes through are coherent.h's
+// (ld_relaxed, st_dev, wait_stores), with what they rest on.
 __device__ __forceinline__ unsigned long long pack2(uint32_t lo, uint32_t hi) {
   return (unsigned long long)lo | ((unsigned long long)hi << 32);
 }
@@ -1038,11 +1015,6 @@ __device__ __forceinline__ CurRec ld_cur(const CurRec* p) {
   r.node = (uint32_t)b;
   r.hist = (uint32_t)(b >> 32);
   return r;
-}
-// Waits until this wave's stores are complete (acknowledged at device
-// scope); the memory clobber keeps the compiler from moving them past it.
-__device__ __forceinline__ void wait_stores() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Upper bound on spin iterations of a wait (each sleeps ~64 cycles): far
