@@ -252,7 +252,8 @@ struct Ctl {
   uint32_t pad1[32];
   // the shared step, written by the leader before `go`
   uint32_t t, W, n_par, nS;
-  uint32_t sel_which, cur_which, status, pad2;
+  uint32_t sel_which, cur_which, status;
+  uint32_t hist_n;  // history records written before the step
   // pushes of the step into `next` (low 32 bits) and `selected` (high 32
   // bits): one 64-bit atomic add a workgroup
   unsigned long long pushes;

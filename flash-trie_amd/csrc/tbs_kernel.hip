@@ -1812,6 +1812,40 @@ __device__ __forceinline__ void helper_loop(const KArgs& a, const DevReq& d, uin
     wait_stores();  // this slice's pushes and counters are complete
     __syncthreads();
     if (tid == 0) st_dev(dw, v);  // then its done word: no shared counter
+    // The helper that shares the leader's XCD -- blocks are dealt to the 8
+    // XCDs in turn, so block req + g * batch sits with the leader's when
+    // g * batch is a multiple of 8 -- reads a word of every 64 bytes of the
+    // request's rows after the next one and of the history records written
+    // so far, so that the leader's later reads of them (the single-wave
+    // tail's row fills, the output's history walks) find them in their L2.
+    // A streamed request's later rows only once their copy to the device
+    // stage is done (before, the lines could be stale); the history is the
+    // leader's, written through the same L2.
+    const uint32_t pfg = (a.batch & 7u) == 0 ? 1u
+                         : (a.batch & 3u) == 0 ? 2u
+                         : (a.batch & 1u) == 0 ? 4u : 8u;
+    if (g == pfg && t + 2u < d.T && !big) {
+      bool ready = true;
+      if constexpr (kStreamed) {
+        if (stream_split(a.head_rows, d.T, d.K) < d.T) {
+          const unsigned long long c = ld_relaxed(&ctl->copy);
+          ready = (c >> 32) == a.epoch && ((uint32_t)c & kCopyDone);
+        }
+      }
+      if (ready) {
+        const uint64_t r0 = (uint64_t)(t + 2u) * d.K;
+        const uint32_t n = (d.T - t - 2u) * d.K;  // words of each array
+        const HistRec* hist = (const HistRec*)(ws + a.lay.hist);
+        const uint32_t nh = min(ld_relaxed(&ctl->hist_n), a.lay.hist_cap);
+        uint32_t acc = 0;
+        for (uint32_t i = tid * 16u; i < n; i += kBlock * 16u)
+          acc ^= rid[r0 + i] ^ __float_as_uint(rlp[r0 + i]);
+        for (uint32_t i = tid * 4u; i < nh; i += kBlock * 4u) acc ^= hist[i].tok;
+        // (a use of the loads, so that they stay: the slice's counter, already
+        // reported in the done word and cleared before the next slice)
+        if (acc == 0x9E3779B9u) sm.w_probes = acc;
+      }
+    }
   }
 }
 
@@ -2471,6 +2505,7 @@ __global__ void __launch_bounds__(kBlock) tbs_kernel(KArgs a) {
         st_dev(&ctl->nS, nS);
         st_dev(&ctl->sel_which, sel_which);
         st_dev(&ctl->cur_which, cur_which);
+        st_dev(&ctl->hist_n, hist_used);
       }
       wait_stores();  // the step's data is complete before `go` moves
       __syncthreads();
