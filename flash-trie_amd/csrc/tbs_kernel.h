@@ -257,7 +257,10 @@ struct Ctl {
   // pushes of the step into `next` (low 32 bits) and `selected` (high 32
   // bits): one 64-bit atomic add a workgroup
   unsigned long long pushes;
-  unsigned long long pad4[2];
+  // streamed search: (launch epoch << 32) | 1 once the leader has copied
+  // the request's first rows to the device stage
+  unsigned long long head;
+  unsigned long long pad4;
   // streamed search: the copy of the rows after the first ready word's
   // (launch epoch << 32) | kCopy* state, claimed by helper 1 or the leader
   unsigned long long copy;
