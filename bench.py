@@ -2,7 +2,7 @@
 """Trie beam search benchmark on one MI355X.
 
 The reference publishes its latency at the C++ boundary and its throughput
-at harness wall time (BASELINE: README.md:48-64; tools/bindings.cpp:90-100;
+at harness wall time (its README.md:48-64; tools/bindings.cpp:90-100;
 examples/run_trie_search.py:189-199).  Both are measured here, each at its
 own boundary, with the reference's protocol (examples/flashtrie_bench.py:
 270-291): per configuration one warm-up pass and --passes measured passes
