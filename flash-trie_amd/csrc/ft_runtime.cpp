@@ -1364,15 +1364,26 @@ static KArgs kernel_args(const ft_ctx* c, const uint8_t* stage, size_t first, si
   return a;
 }
 
-// One launch of the search kernel on the context stream, bracketed by a pair of the
-// ring's timing events.
-static int launch_timed(ft_ctx* c, const KArgs& a) {
+// One launch of the search kernel on the context stream, timed by a pair of
+// the ring's events.  `attached`: events attached to the dispatch, the
+// kernel's own run as a kernel trace reports it (the device-resident
+// launches, whose durations ft_launch_times reports).  Otherwise markers
+// recorded around the launch, which also span the ~5 us the queue spends
+// between them and the kernel: the streamed search keeps these, because an
+// attached pair made its calls ~16 us slower at the C++ boundary.
+static int launch_timed(ft_ctx* c, const KArgs& a, bool attached) {
   (void)hipSetDevice(c->device);
   const size_t slot = (c->launches % ft_ctx::kRing) * 2;
-  (void)hipEventRecord(c->ring[slot], c->stream);
-  hipError_t e = launch_tbs(a, c->stream);
-  if (e != hipSuccess) return hip_fail(e, "launch of the search kernel");
-  (void)hipEventRecord(c->ring[slot + 1], c->stream);
+  hipError_t e;
+  if (attached) {
+    e = launch_tbs(a, c->stream, c->ring[slot], c->ring[slot + 1]);
+    if (e != hipSuccess) return hip_fail(e, "launch of the search kernel");
+  } else {
+    (void)hipEventRecord(c->ring[slot], c->stream);
+    e = launch_tbs(a, c->stream);
+    if (e != hipSuccess) return hip_fail(e, "launch of the search kernel");
+    (void)hipEventRecord(c->ring[slot + 1], c->stream);
+  }
   ++c->launches;
   return FT_OK;
 }
@@ -1393,7 +1404,7 @@ int ft_launch_range(ft_ctx* c, size_t first, size_t count) {
   for (size_t i = first; i < first + count; ++i) kmax = std::max(kmax, c->staged[i].K);
   const KArgs a = kernel_args(c, c->d_stage, first, count, kmax, c->d_ws, c->ws_stride,
                               c->lay, c->d_out, c->out_stride);
-  if (int rc = launch_timed(c, a)) return rc;
+  if (int rc = launch_timed(c, a, true)) return rc;
   c->launched = true;
   for (size_t i = first; i < first + count; ++i) c->launched_slot[i] = 1;
   return FT_OK;
@@ -1694,7 +1705,7 @@ int ft_search_each(ft_ctx* c, const ft_request* reqs, size_t batch, ft_result* r
   // the result headers start unpublished
   for (size_t r = 0; r < batch; ++r)
     __atomic_store_n(&((OutHeader*)(c->h_out + c->out_stride * r))->status, 0u, __ATOMIC_RELAXED);
-  if (int rc = launch_timed(c, a)) return drop(rc);
+  if (int rc = launch_timed(c, a, false)) return drop(rc);
   PackJob job;
   job.reqs = reqs;
   job.D = D;
@@ -1888,7 +1899,7 @@ int ft_search_noalloc(ft_ctx* c, const ft_request* reqs, size_t batch,
     return hip_fail(e, "clear_controls");
   const KArgs a = kernel_args(c, base, 0, batch, (uint32_t)K, base + ws_off, ws_stride, L,
                               base + out_off, out_stride);
-  if (int rc = launch_timed(c, a)) return rc;
+  if (int rc = launch_timed(c, a, false)) return rc;
   if ((e = hipMemcpyAsync(g_na_out, base + out_off, out_stride * batch, hipMemcpyDeviceToHost,
                           c->stream)) != hipSuccess)
     return hip_fail(e, "hipMemcpyAsync(scratch output)");

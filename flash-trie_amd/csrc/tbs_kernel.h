@@ -351,7 +351,10 @@ constexpr uint32_t kLoudsBlockBits = 512;
 // Launches the search over `batch` requests (wgs workgroups each) on
 // `stream` (an ordinary launch: no workgroup waits for one that may not be
 // resident, see tbs_kernel.hip).
-hipError_t launch_tbs(const KArgs& args, hipStream_t stream);
+// (start / stop, when given, are updated with the kernel's own start and
+// stop times: events attached to its dispatch, not markers around it)
+hipError_t launch_tbs(const KArgs& args, hipStream_t stream, hipEvent_t start = nullptr,
+                      hipEvent_t stop = nullptr);
 
 // Fills the root directory `dir` (root_n entries, zeroed by the caller)
 // from the root's `deg` children starting at node c0, on `stream`.  `args`

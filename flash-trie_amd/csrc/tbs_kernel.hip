@@ -35,6 +35,7 @@
 // Scores: s is the f64 sum of f32 logps (agent.cc:36); norm = s * lnf[|Q|]
 // with lnf[d] = pow(6 / (5 + d), alpha) computed on the host with the same
 // libm call as the reference (agent.h:69-72), so norms are bit-identical.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -3220,15 +3221,19 @@ hipError_t clear_controls(uint8_t* ws, uint64_t stride, uint64_t ctl_off, uint64
 // workgroup wait for one that is not running (helpers' slices are claimed,
 // and the leader takes over the slices no helper has claimed), so the grid
 // needs no co-residency guarantee.
-hipError_t launch_tbs(const KArgs& args, hipStream_t stream) {
+hipError_t launch_tbs(const KArgs& args, hipStream_t stream, hipEvent_t start,
+                      hipEvent_t stop) {
   const dim3 grid(args.batch * args.wgs), block(kBlock);
   if (args.louds_words) {
     if (args.ready) return hipErrorInvalidValue;  // (no streamed LOUDS search)
-    hipLaunchKernelGGL((tbs_kernel<true, false>), grid, block, 0, stream, args);
+    hipExtLaunchKernelGGL((tbs_kernel<true, false>), grid, block, 0, stream, start, stop, 0,
+                          args);
   } else if (args.ready) {
-    hipLaunchKernelGGL((tbs_kernel<false, true>), grid, block, 0, stream, args);
+    hipExtLaunchKernelGGL((tbs_kernel<false, true>), grid, block, 0, stream, start, stop, 0,
+                          args);
   } else {
-    hipLaunchKernelGGL((tbs_kernel<false, false>), grid, block, 0, stream, args);
+    hipExtLaunchKernelGGL((tbs_kernel<false, false>), grid, block, 0, stream, start, stop, 0,
+                          args);
   }
   return hipGetLastError();
 }

@@ -186,8 +186,11 @@ int ft_reserve_staging(ft_ctx* ctx, size_t max_staged);
  * (async). */
 int ft_launch_range(ft_ctx* ctx, size_t first, size_t count);
 
-/* Kernel durations (HIP events) of the last n launches, oldest first;
- * waits for the stream.  At most 1024 are kept. */
+/* Kernel durations of the last n launches, oldest first; waits for the
+ * stream.  At most 1024 are kept.  A launch of staged requests
+ * (ft_launch, ft_launch_range) is timed by HIP events attached to its
+ * dispatch (its start to its end); a streamed search (ft_search) by events
+ * recorded around it, which also span the queue's time between them. */
 int ft_launch_times(ft_ctx* ctx, double* ms, size_t n);
 
 /* Waits for the last launch, copies results back, fills `results`.  A

@@ -12,7 +12,7 @@
 #include <random>
 
 namespace ftk {  // the device side is not linked here
-hipError_t launch_tbs(const KArgs&, hipStream_t) { return hipErrorUnknown; }
+hipError_t launch_tbs(const KArgs&, hipStream_t, hipEvent_t, hipEvent_t) { return hipErrorUnknown; }
 hipError_t launch_root_dir(const KArgs&, RootEnt*, uint32_t, uint32_t, uint32_t, hipStream_t) {
   return hipErrorUnknown;
 }
